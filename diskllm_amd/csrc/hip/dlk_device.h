@@ -1,0 +1,81 @@
+/*
+ * dlk_device.h -- device helpers shared by the sampling kernels (gfx950, wave64).
+ */
+#ifndef DLK_DEVICE_H
+#define DLK_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "expf_glibc.h"
+
+#define DLK_DEV __device__ __forceinline__
+
+namespace dlk {
+
+constexpr int kWave = 64;
+
+DLK_DEV int lane_id() { return __lane_id(); }
+DLK_DEV int wave_id() { return threadIdx.x >> 6; }
+DLK_DEV int n_waves() { return blockDim.x >> 6; }
+
+DLK_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
+DLK_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
+DLK_DEV uint64_t d2u(double d) { return (uint64_t)__double_as_longlong(d); }
+DLK_DEV double u2d(uint64_t u) { return __longlong_as_double((long long)u); }
+
+DLK_DEV uint64_t ballot(bool p) { return __ballot(p); }
+DLK_DEV int first_lane(uint64_t m) { return m ? __builtin_ctzll(m) : 64; }
+
+template <class T>
+DLK_DEV T shfl(T v, int src) { return __shfl(v, src, 64); }
+template <class T>
+DLK_DEV T shfl_up(T v, int d) { return __shfl_up(v, (unsigned)d, 64); }
+template <class T>
+DLK_DEV T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+
+/* Orderable descending key of a float: ascending key <=> descending value, with
+ * -0 and +0 made equal (C's '<' treats them as equal, src/sampler.c:114,:122). */
+DLK_DEV uint32_t desc_key(float s) {
+    uint32_t u = f2u(s);
+    if (u == 0x80000000u) u = 0;
+    uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ~ord;
+}
+DLK_DEV float key_value(uint32_t key) {
+    uint32_t ord = ~key;
+    return u2f((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+
+/* Round-to-nearest-even conversion of an integer v < 2^53 to float, written out
+ * so it does not depend on the compiler's u64->f32 lowering. */
+DLK_DEV float u53_to_f32_rn(uint64_t v) {
+    if (v == 0) return 0.0f;
+    int msb = 63 - __clzll((long long)v);
+    if (msb <= 23) return (float)(uint32_t)v;
+    int sh = msb - 23;
+    uint64_t mant = v >> sh;
+    uint64_t rem = v & ((1ull << sh) - 1);
+    uint64_t half = 1ull << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1))) mant++;
+    return ldexpf((float)(uint32_t)mant, sh);
+}
+
+/* xorshift64 + rand_f32, src/sampler.c:69-81. */
+DLK_DEV uint64_t xorshift64(uint64_t x) {
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return x;
+}
+DLK_DEV float rand_f32_from(uint64_t x) { return u53_to_f32_rn(x >> 11) * (1.0f / 9007199254740992.0f); }
+
+/* Wave-wide sum (any order) of a double. */
+DLK_DEV double wave_sum(double v) {
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+
+}  // namespace dlk
+
+#endif

@@ -1,0 +1,321 @@
+/*
+ * exact_scan.h -- bit-exact emulation of a sequential floating-point running sum
+ * on one wavefront, with the bulk of the work done in parallel.
+ *
+ * The reference accumulates probabilities one at a time (src/sampler.c:177-181,
+ * :198-199, :207-215, :218-219 in double; :226-232 in float).  A tree or
+ * prefix sum rounds differently, and the sampled token depends on those bits,
+ * so the order-dependent sum has to be reproduced exactly.
+ *
+ * Method.  Let the running value c lie in binade b, i.e. c in [2^b, 2^(b+1))
+ * (the lowest binade also holds 0 and the subnormals, which share its grid), and
+ * let u = 2^(b - MB + 1) be its ulp, MB = 24 (float) or 53 (double).  Then c = m*u
+ * for an integer m < 2^MB, and for a non-negative float q whose sum stays in the
+ * binade, fl(c + q) = u * RNE(m + q/u) = u * (m + n(q, m mod 2)): n is q/u rounded
+ * to nearest, and only when q/u is exactly halfway does the result depend on m's
+ * parity (ties go to the even m).  So inside one binade the sum is an integer
+ * prefix sum over pair-valued increments (A0, A1) -- the increment for an even and
+ * an odd start -- and pairs compose associatively:
+ *      (A then B)_p = A_p + B_{(p + A_p) mod 2}.
+ * A step that leaves the binade (m + n >= 2^MB) is done as a real IEEE addition.
+ *
+ * Data.  The block precomputes aggregates per chunk (64 elements) and per group
+ * (64 chunks = 4096 elements), each under a *predicted* binade taken from an
+ * approximate prefix sum (wrong predictions only cost time: the resolver checks
+ * every aggregate against the true binade and descends into it otherwise).
+ *
+ * Resolve.  One wave walks the sequence: 64 aggregates (or elements) per step,
+ * an inclusive pair scan across lanes, and a ballot for the first lane whose
+ * aggregate is invalid for the current binade, leaves the binade, or crosses the
+ * caller's threshold; it advances to that lane and descends one level, down to
+ * single elements, where exits become real additions.  Every step consumes at
+ * least one element or descends one of three levels, so the walk ends.
+ *
+ * Thresholds.  A threshold v stops the walk at the first element after which
+ * c >= v (the draw r < cumul uses v = nextafter(r); top-p (float)cumul >= top_p
+ * uses the smallest double that rounds to >= top_p).  In binade b this is the
+ * integer test m >= ceil(v / u).
+ */
+#ifndef DLK_EXACT_SCAN_H
+#define DLK_EXACT_SCAN_H
+
+#include "dlk_device.h"
+
+namespace dlk {
+
+constexpr uint64_t kCap = 1ull << 62;       /* saturation: far above any binade */
+constexpr int kInvalidBinade = 0x7fff;
+
+struct Pair {
+    uint64_t a0, a1;
+};
+
+DLK_DEV uint64_t sat_add(uint64_t a, uint64_t b) {
+    uint64_t s = a + b;                      /* a, b <= 2^62: no wrap */
+    return s > kCap ? kCap : s;
+}
+
+DLK_DEV Pair compose(Pair A, Pair B) {
+    Pair C;
+    C.a0 = sat_add(A.a0, (A.a0 & 1) ? B.a1 : B.a0);
+    C.a1 = sat_add(A.a1, (A.a1 & 1) ? B.a0 : B.a1);
+    return C;
+}
+
+template <int MB>
+struct Fmt;
+template <>
+struct Fmt<24> {
+    static constexpr int EMIN = -126;
+    using T = float;
+};
+template <>
+struct Fmt<53> {
+    static constexpr int EMIN = -1022;
+    using T = double;
+};
+
+/* Increment of a non-negative float q on the grid 2^ue. */
+DLK_DEV Pair increment(float q, int ue) {
+    uint32_t u = f2u(q);
+    uint32_t ex = u >> 23;
+    uint32_t mq = u & 0x7fffffu;
+    int eq;
+    if (ex == 0) {
+        eq = -149;
+    } else {
+        mq |= 0x800000u;
+        eq = (int)ex - 150;
+    }
+    if (mq == 0) return Pair{0, 0};
+    int sh = eq - ue;
+    if (sh >= 0) {
+        uint64_t n = sh >= 38 ? kCap : ((uint64_t)mq << sh);
+        return Pair{n, n};
+    }
+    int s = -sh;
+    if (s >= 26) return Pair{0, 0};          /* q/u < 1/4 */
+    uint64_t n = mq >> s;
+    uint32_t rem = mq & ((1u << s) - 1u);
+    uint32_t half = 1u << (s - 1);
+    if (rem > half) n += 1;
+    if (rem == half) return Pair{n + (n & 1), n + ((n + 1) & 1)};
+    return Pair{n, n};
+}
+
+/* Binade of a running value / its integer significand on that binade's grid. */
+DLK_DEV void split(float c, int &b, uint64_t &m) {
+    uint32_t u = f2u(c), ex = u >> 23;
+    if (ex <= 1) { b = -126; m = u; }
+    else { b = (int)ex - 127; m = (u & 0x7fffffu) | 0x800000u; }
+}
+DLK_DEV void split(double c, int &b, uint64_t &m) {
+    uint64_t u = d2u(c), ex = u >> 52;
+    if (ex <= 1) { b = -1022; m = u; }
+    else { b = (int)ex - 1023; m = (u & 0xfffffffffffffull) | (1ull << 52); }
+}
+DLK_DEV float join_f(int b, uint64_t m) {
+    if (m >= (1ull << 24)) return u2f((uint32_t)(b + 128) << 23);   /* exactly 2^(b+1) */
+    if (b == -126) return u2f((uint32_t)m);
+    return u2f(((uint32_t)(b + 127) << 23) | ((uint32_t)m & 0x7fffffu));
+}
+DLK_DEV double join_d(int b, uint64_t m) {
+    if (m >= (1ull << 53)) return u2d((uint64_t)(b + 1024) << 52);
+    if (b == -1022) return u2d(m);
+    return u2d(((uint64_t)(b + 1023) << 52) | (m & 0xfffffffffffffull));
+}
+template <int MB>
+DLK_DEV typename Fmt<MB>::T join(int b, uint64_t m);
+template <>
+DLK_DEV float join<24>(int b, uint64_t m) { return join_f(b, m); }
+template <>
+DLK_DEV double join<53>(int b, uint64_t m) { return join_d(b, m); }
+
+/* Predicted binade of a running value approximated by the double v >= 0. */
+template <int MB>
+DLK_DEV int predict_binade(double v) {
+    uint64_t u = d2u(v);
+    int ex = (int)(u >> 52) - 1023;
+    return ex <= Fmt<MB>::EMIN ? Fmt<MB>::EMIN : ex;
+}
+
+/* Smallest integer t with t * 2^ue >= v (v >= 0 finite double); saturating. */
+DLK_DEV uint64_t ceil_div_pow2(double v, int ue) {
+    uint64_t u = d2u(v);
+    uint64_t ex = u >> 52, mv = u & 0xfffffffffffffull;
+    if (ex == 0 && mv == 0) return 0;
+    int ev;
+    if (ex == 0) ev = -1074;
+    else { mv |= 1ull << 52; ev = (int)ex - 1075; }
+    int sh = ev - ue;
+    if (sh >= 0) return sh >= 9 ? kCap : (mv << sh);
+    int s = -sh;
+    if (s >= 64) return 1;
+    return (mv >> s) + ((mv & ((1ull << s) - 1)) != 0);
+}
+
+DLK_DEV Pair wave_incl_scan(Pair x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        uint64_t l0 = shfl_up(x.a0, d), l1 = shfl_up(x.a1, d);
+        if (lane >= d) x = compose(Pair{l0, l1}, x);
+    }
+    return x;
+}
+
+/* Aggregates of one sequence: chunk (64) and group (4096) level.  Flat
+ * pointers, so they may live in LDS or in global memory. */
+struct Aggs {
+    uint64_t *a0, *a1;
+    int *bh;
+    uint64_t *ga0, *ga1;
+    int *gbh;
+    double *P;      /* [nch + 1] approximate prefix sums at chunk starts */
+};
+
+/* Block-wide: P[c] = approximate exclusive prefix of q over chunks, P[nch] = total.
+ * Uses `red` (>= blockDim/64 doubles of LDS) as scratch. */
+template <class QF>
+__device__ void chunk_prefix(int n, const QF &q, double *P, double *red) {
+    const int lane = lane_id(), w = wave_id(), nw = n_waves();
+    const int nch = (n + 63) >> 6;
+    for (int c = w; c < nch; c += nw) {
+        int i = c * 64 + lane;
+        double v = i < n ? (double)q(i) : 0.0;
+        v = wave_sum(v);
+        if (lane == 0) P[c] = v;
+    }
+    __syncthreads();
+    /* exclusive scan over nch values: each thread a contiguous run. */
+    const int T = blockDim.x, t = threadIdx.x;
+    const int per = (nch + T - 1) / T;
+    const int b0 = t * per, b1 = min(nch, b0 + per);
+    double loc = 0.0;
+    for (int c = b0; c < b1; c++) loc += P[c];
+    double inc = loc;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        double o = shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    double wbase = 0.0;
+    for (int k = 0; k < w; k++) wbase += red[k];
+    double run = wbase + inc - loc;
+    __syncthreads();
+    for (int c = b0; c < b1; c++) { double v = P[c]; P[c] = run; run += v; }
+    if (t == T - 1) P[nch] = run;
+    __syncthreads();
+}
+
+/* Block-wide: chunk and group aggregates of q under binades predicted from
+ * scale * min(P, cut). */
+template <int MB, class QF>
+__device__ void build_aggs(int n, const QF &q, const Aggs &A, double scale, double cut) {
+    const int lane = lane_id(), w = wave_id(), nw = n_waves();
+    const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
+    for (int c = w; c < nch; c += nw) {
+        int bs = predict_binade<MB>(fmin(A.P[c], cut) * scale);
+        int be = predict_binade<MB>(fmin(A.P[c + 1], cut) * scale);
+        if (bs != be) {
+            if (lane == 0) A.bh[c] = kInvalidBinade;
+            continue;
+        }
+        int i = c * 64 + lane;
+        Pair x = i < n ? increment(q(i), bs - (MB - 1)) : Pair{0, 0};
+        x = wave_incl_scan(x, lane);
+        if (lane == 63) { A.a0[c] = x.a0; A.a1[c] = x.a1; A.bh[c] = bs; }
+    }
+    __syncthreads();
+    for (int g = w; g < ngr; g += nw) {
+        int c = g * 64 + lane;
+        bool in = c < nch;
+        int b0 = A.bh[g * 64];
+        bool ok = !in || A.bh[c] == b0;
+        ok = (ballot(!ok) == 0) && b0 != kInvalidBinade;
+        if (!ok) {
+            if (lane == 0) A.gbh[g] = kInvalidBinade;
+            continue;
+        }
+        Pair x = in ? Pair{A.a0[c], A.a1[c]} : Pair{0, 0};
+        x = wave_incl_scan(x, lane);
+        if (lane == 63) { A.ga0[g] = x.a0; A.ga1[g] = x.a1; A.gbh[g] = b0; }
+    }
+    __syncthreads();
+}
+
+template <int MB>
+struct ResolveOut {
+    int pos;                        /* first element reaching the threshold, or -1 */
+    typename Fmt<MB>::T value;      /* running value after `pos` (or after the last element) */
+};
+
+/* One wave: walk the sequence with the aggregates.  has_thr selects a stop at
+ * the first element after which c >= thr_v.  All lanes return the same result. */
+template <int MB, class QF>
+__device__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs &A, bool has_thr, double thr_v) {
+    using T = typename Fmt<MB>::T;
+    const int lane = lane_id();
+    const uint64_t top = 1ull << MB;
+    const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
+    int b = Fmt<MB>::EMIN;
+    uint64_t m = 0;
+    uint64_t thr = has_thr ? ceil_div_pow2(thr_v, b - (MB - 1)) : kCap;
+    int pos = 0, cap = 2;
+    while (pos < n) {
+        int L = 0;
+        if (cap >= 2 && (pos & 4095) == 0) L = 2;
+        else if (cap >= 1 && (pos & 63) == 0) L = 1;
+        int item = pos >> (6 * L), count;
+        if (L == 2) count = min(64, ngr - item);
+        else if (L == 1) count = min(64 - (item & 63), nch - item);
+        else count = min(64 - (pos & 63), n - pos);
+        const bool act = lane < count;
+        Pair x{0, 0};
+        bool valid = true;
+        float qv = 0.0f;
+        if (act) {
+            if (L == 0) {
+                qv = q(pos + lane);
+                x = increment(qv, b - (MB - 1));
+            } else if (L == 1) {
+                int c = item + lane;
+                valid = A.bh[c] == b;
+                x = Pair{A.a0[c], A.a1[c]};
+            } else {
+                int g = item + lane;
+                valid = A.gbh[g] == b;
+                x = Pair{A.ga0[g], A.ga1[g]};
+            }
+        }
+        if (!valid) x = Pair{0, 0};
+        x = wave_incl_scan(x, lane);
+        uint64_t ma = sat_add(m, (m & 1) ? x.a1 : x.a0);
+        bool ev = act && (!valid || ma >= top || ma >= thr);
+        int f = first_lane(ballot(ev));
+        if (f > count) f = count;
+        if (f > 0) m = shfl(ma, f - 1);
+        pos = min(n, pos + (f << (6 * L)));
+        if (f == count) { cap = 2; continue; }
+        if (L > 0) { cap = L - 1; continue; }
+        /* element event at pos: leave the binade with a real addition, or stop. */
+        uint64_t maf = shfl(ma, f);
+        float qf = shfl(qv, f);
+        cap = 2;
+        if (maf >= top) {
+            T c = join<MB>(b, m) + (T)qf;
+            if (has_thr && (double)c >= thr_v) return ResolveOut<MB>{pos, c};
+            split(c, b, m);
+            thr = has_thr ? ceil_div_pow2(thr_v, b - (MB - 1)) : kCap;
+            pos += 1;
+        } else {
+            return ResolveOut<MB>{pos, join<MB>(b, maf)};
+        }
+    }
+    return ResolveOut<MB>{-1, join<MB>(b, m)};
+}
+
+}  // namespace dlk
+
+#endif

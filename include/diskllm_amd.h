@@ -1,0 +1,103 @@
+/*
+ * diskllm_amd.h -- batched, device-resident C ABI of the MI355X sampling and
+ * grammar-mask path.
+ *
+ * The drop-in headers include/sampler.h and include/grammar.h keep DiskLLM's
+ * single-row host API; this header adds the batched entry points they are built
+ * on.  All pointers below are device pointers unless stated otherwise; every
+ * call is asynchronous on `stream` and returns a DLK_* status.
+ *
+ * Row semantics are those of the reference caller diskllm_sample_grammar()
+ * (src/core/sampler_api.c:48-73) with the allow-mask in place of the grammar
+ * callback: mask -> penalties (in `penalty_order`) -> sampler_sample()
+ * (src/sampler.c:136-234).  Token ids are bit-identical to the reference built
+ * as strict ISO C (-std=c11 -O2) on the same inputs and the same xorshift state.
+ */
+#ifndef DISKLLM_AMD_H
+#define DISKLLM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DLK_OK 0
+#define DLK_ERR_INVALID (-1)      /* bad argument */
+#define DLK_ERR_UNSUPPORTED (-2)  /* shape or parameter outside the supported range */
+#define DLK_ERR_HIP (-3)          /* a HIP runtime call failed */
+
+/* Device status bits written by the kernels (dlk_batch.status). */
+#define DLK_STATUS_HISTORY_TOO_LONG 1u
+
+/* Penalty ops, packed low nibble first into dlk_sample_params.penalty_order. */
+#define DLK_OP_REPETITION 1u  /* src/sampler.c:21-33, once per occurrence */
+#define DLK_OP_FREQUENCY 2u   /* builder-defined: l -= f * count, once per distinct id */
+#define DLK_OP_PRESENCE 3u    /* src/sampler.c:35-52, once per distinct id */
+/* Reference caller order: presence then repetition (src/core/sampler_api.c:55-61). */
+#define DLK_ORDER_REFERENCE (DLK_OP_PRESENCE | (DLK_OP_REPETITION << 4))
+/* repetition -> frequency -> presence. */
+#define DLK_ORDER_REP_FREQ_PRES (DLK_OP_REPETITION | (DLK_OP_FREQUENCY << 4) | (DLK_OP_PRESENCE << 8))
+
+typedef struct {
+    /* sampler_config (include/sampler.h:10-16) without the seed: */
+    float temperature;        /* 0 = greedy; otherwise 1/temperature must be finite and > 0 */
+    int top_k;                /* active when 0 < top_k < vocab; at most 4096 */
+    float top_p;              /* active when < 1 */
+    float min_p;              /* active when > 0 (absolute threshold, src/sampler.c:189) */
+    /* penalties (diskllm_sampler_params, include/diskllm.h:48-56, plus frequency): */
+    float repeat_penalty;     /* active when > 1 */
+    float frequency_penalty;  /* active when != 0 */
+    float presence_penalty;   /* active when != 0 */
+    uint32_t penalty_order;   /* DLK_ORDER_* or any packing of DLK_OP_* */
+    int max_history;          /* upper bound on any row's history length (LDS sizing) */
+    int n_out;                /* candidate outputs per row (0 = none) */
+} dlk_sample_params;
+
+typedef struct {
+    const float *logits;      /* [rows, ld] fp32, read only */
+    int64_t ld;               /* row stride in elements (>= vocab) */
+    const int32_t *hist_off;  /* [rows+1] CSR offsets into hist_ids, or NULL */
+    const int32_t *hist_ids;  /* previously seen token ids (out-of-range ids are skipped) */
+    const uint32_t *mask;     /* packed allow-masks, bit i%32 of word i/32 (1 = allowed), or NULL */
+    int64_t mask_ld;          /* words between mask rows */
+    const int32_t *mask_row;  /* [rows] mask row used by each row (e.g. a DFA state), or NULL = row */
+    uint64_t *rng;            /* [rows] xorshift64 states (non-zero), advanced once per sampled row */
+    int32_t *out_ids;         /* [rows] sampled token ids */
+    int32_t *out_cand_ids;    /* [rows, n_out] first n_out candidates in buffer order, or NULL */
+    float *out_cand_probs;    /* [rows, n_out] their softmax probabilities (src/sampler.c:183-185) */
+    float *out_cand_logprobs; /* [rows, n_out] log of their final sampling probability (-inf if cut) */
+    uint32_t *status;         /* one word of DLK_STATUS_* bits, OR-ed by the kernels, or NULL */
+} dlk_batch;
+
+/* Initial xorshift state for a seed (src/sampler.c:87): seed 0 -> 0xDEADBEEF12345678. */
+uint64_t dlk_seed_state(uint64_t seed);
+
+/* Sample one token per row.  Replaces, for a batch of rows, the sequence
+ * diskllm_grammar_apply_mask (as a packed mask) -> sampler_apply_*_penalty ->
+ * sampler_sample of the reference (src/core/sampler_api.c:48-63). */
+int dlk_sample(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
+               hipStream_t stream);
+
+/* Byte-DFA allow-masks (no reference counterpart; replaces the accept_str
+ * callback loop of src/core/grammar.c:284-306 for byte-level automata).
+ * Token t = bytes[off[t] .. off[t+1]) is allowed from state s iff s != 0, the
+ * token is non-empty and no prefix walk through trans[s*256 + byte] reaches
+ * state 0; the EOS id (if >= 0) is allowed iff bit s of accept_mask is set.
+ * Writes out_mask[r * mask_ld + w] for the n_rows states in `states`. */
+int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const uint8_t *trans, int n_states,
+                 const int32_t *states, int n_rows, int eos_id, uint64_t accept_mask, uint32_t *out_mask,
+                 int64_t mask_ld, hipStream_t stream);
+
+/* y[i] = expf(x[i]) for i < n, bit-identical to the host libm expf that the
+ * reference's softmax calls (src/sampler.c:179; glibc 2.35, x86-64 FMA variant). */
+int dlk_expf(const float *x, float *y, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
