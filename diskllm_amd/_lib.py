@@ -19,6 +19,7 @@ DLK_ERR_INVALID = -1
 DLK_ERR_UNSUPPORTED = -2
 DLK_ERR_HIP = -3
 DLK_STATUS_HISTORY_TOO_LONG = 1
+PATH_AUTO, PATH_ROW = 0, 1
 
 OP_REPETITION, OP_FREQUENCY, OP_PRESENCE = 1, 2, 3
 ORDER_REFERENCE = OP_PRESENCE | (OP_REPETITION << 4)
@@ -28,7 +29,8 @@ ORDER_REP_FREQ_PRES = OP_REPETITION | (OP_FREQUENCY << 4) | (OP_PRESENCE << 8)
 class SampleParams(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
                 ("repeat_penalty", C.c_float), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float),
-                ("penalty_order", C.c_uint32), ("max_history", C.c_int), ("n_out", C.c_int)]
+                ("penalty_order", C.c_uint32), ("max_history", C.c_int), ("n_out", C.c_int),
+                ("path", C.c_int)]
 
 
 class Batch(C.Structure):

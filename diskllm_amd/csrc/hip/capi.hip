@@ -8,9 +8,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "sampler_params.h"
+#include "sampler_topk.h"
 
 extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t lds_bytes, hipStream_t stream);
+extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 
 namespace {
 
@@ -37,6 +41,97 @@ double topp_threshold(float tp) {
     double mid = ((double)lo + (double)tp) * 0.5;
     if ((float)mid >= tp) return mid;
     return nextafter(mid, INFINITY);
+}
+
+/* One lazily grown workspace per device: a zero-initialised counter region that
+ * only the kernels' counter protocol writes (each counter is back at zero when a
+ * launch finishes), then a scratch region.  Calls that overlap on one device must
+ * not share it (use one stream). */
+struct DeviceWorkspace {
+    void *ptr = nullptr;
+    size_t ctr_cap = 0;     /* counters */
+    size_t data_bytes = 0;  /* scratch bytes after the counters */
+};
+std::mutex g_ws_mu;
+DeviceWorkspace g_ws[64];
+
+struct WsView {
+    uint32_t *counters;
+    unsigned char *data;
+};
+
+bool workspace(size_t counters, size_t data_bytes, WsView &out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    DeviceWorkspace &w = g_ws[dev];
+    if (w.ctr_cap < counters || w.data_bytes < data_bytes) {
+        size_t cc = w.ctr_cap > counters ? w.ctr_cap : counters;
+        if (cc < 4096) cc = 4096;
+        cc = (cc + 63) & ~(size_t)63;
+        size_t db = w.data_bytes > data_bytes ? w.data_bytes : data_bytes;
+        if (db < (1u << 20)) db = 1u << 20;
+        if (w.ptr) {
+            if (hipDeviceSynchronize() != hipSuccess) return false;
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.ctr_cap = w.data_bytes = 0;
+        }
+        if (hipMalloc(&w.ptr, cc * 4 + db) != hipSuccess) { w.ptr = nullptr; return false; }
+        if (hipMemset(w.ptr, 0, cc * 4 + db) != hipSuccess) return false;
+        w.ctr_cap = cc;
+        w.data_bytes = db;
+    }
+    out.counters = (uint32_t *)w.ptr;
+    out.data = (unsigned char *)w.ptr + w.ctr_cap * 4;
+    return true;
+}
+
+size_t fixed_lds(const dlk::LdsPlan &pl) {
+    return r16(32 * 8) + r16(64 * 8) + r16(16 * 8) + r16(64 * 4) + 4 * r16((size_t)pl.hcap * 4) +
+           r16((size_t)pl.flag_words * 4);
+}
+
+/* Single-pass top-k path (sampler_topk.hip): returns DLK_OK, or 1 when the
+ * configuration is outside its range (the caller then uses the row kernel). */
+int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
+    using namespace dlk;
+    const int T = kTopkThreads;
+    if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
+    const int k = p.greedy ? 1 : p.top_k;
+    if (k > 1024) return 1;
+    const int KP = k + 16;
+    int ept = 4, G = 0;
+    const int epts[5] = {64, 32, 16, 8, 4};
+    for (int e : epts) {
+        int g = (vocab + e * T - 1) / (e * T);
+        if ((int64_t)g * KP > 4096) break;
+        ept = e;
+        G = g;
+        if ((int64_t)rows * g >= 1024) break;
+    }
+    if (G == 0 || 3 * G > T) return 1;
+    TopkParams f;
+    memset(&f, 0, sizeof(f));
+    f.p = p;
+    f.G = G;
+    f.S = ept * T;
+    f.KP = KP;
+    int need = G * KP;
+    int bc = 2048;
+    while (bc < need || bc < p.plan.kp + 1024) bc <<= 1;
+    f.buf_cap = bc;
+    size_t lds = fixed_lds(p.plan) + r16((size_t)(f.S / 32) * 4) + r16((size_t)T * 4) + r16(64 * 4) +
+                 r16((size_t)bc * 8) + (p.greedy ? 0 : aggs_bytes(k));
+    if (lds > kMaxLds) return 1;
+    size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
+    size_t n_cand = (size_t)rows * G * KP * 8;
+    WsView ws;
+    if (!workspace((size_t)rows, n_slot + n_cand, ws)) return DLK_ERR_HIP;
+    f.counters = ws.counters;
+    f.slots = (TopkSlot *)ws.data;
+    f.cands = (uint64_t *)(ws.data + n_slot);
+    return dlk_launch_topk_kernel(&f, rows, ept, lds, stream) == 0 ? DLK_OK : DLK_ERR_HIP;
 }
 
 }  // namespace
@@ -79,14 +174,17 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
     int nch = (vocab + 63) / 64;
     pl.flag_words = (nch + 31) / 32;
     pl.kp = p.topk_on ? pow2_at_least(p.top_k, 64) : 0;
-    size_t fixed = r16(32 * 8) + r16(64 * 8) + r16(16 * 8) + r16(64 * 4) + 4 * r16((size_t)pl.hcap * 4) +
-                   r16((size_t)pl.flag_words * 4);
+    size_t fixed = fixed_lds(pl);
     size_t region = 0;
     if (!p.greedy) {
         if (p.topk_on) region = r16((size_t)pl.kp * 8) + (aggs_bytes(p.top_k) > 8192 ? aggs_bytes(p.top_k) : 8192);
         else region = aggs_bytes(vocab);
     }
     size_t total = fixed + region;
+    if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on)) {
+        int rc = launch_topk(p, rows, vocab, stream);
+        if (rc <= 0) return rc;
+    }
     if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;
     pl.bytes = (int)total;
     return dlk_launch_row_kernel(&p, rows, total, stream) == 0 ? DLK_OK : DLK_ERR_HIP;

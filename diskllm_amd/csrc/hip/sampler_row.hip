@@ -3,505 +3,14 @@
  * (penalties -> temperature -> top-k -> softmax -> min-p -> top-p -> draw) for
  * one row of logits, bit-exact with the reference.
  *
- * This kernel is the general path: every configuration runs through it, and the
- * multi-workgroup fast paths fall back to it for rows they cannot certify.  It
- * streams the row from global memory several times (the row stays in L2/MALL
+ * This kernel is the general path: every configuration can run through it, and
+ * the multi-workgroup fast paths fall back to it for rows they cannot certify.
+ * It streams the row from global memory several times (the row stays in L2/MALL
  * after the first pass) and keeps everything else in LDS.
- *
- * Reference map:
- *   penalties          src/sampler.c:21-52 (+ builder frequency), order src/core/sampler_api.c:55-61
- *   packed mask        -INFINITY writes of src/core/grammar.c:285-305
- *   greedy             src/sampler.c:9-19, :140-142
- *   temperature / max  src/sampler.c:153-162
- *   top-k              src/sampler.c:109-134, :165-170 (first k under (value desc, index asc))
- *   softmax            src/sampler.c:172-185
- *   min-p              src/sampler.c:188-202
- *   top-p              src/sampler.c:205-222
- *   draw               src/sampler.c:225-233
  */
-#include <math.h>
-
-#include "dlk_device.h"
-#include "exact_scan.h"
-#include "sampler_params.h"
+#include "sampler_common.h"
 
 namespace dlk {
-
-__constant__ uint64_t kExp2Tab[32] = DLK_EXP2_TAB_INIT;
-
-/* ------------------------------------------------------------------ row view */
-
-struct Row {
-    const float *lg;
-    const uint32_t *mk;      /* packed allow-mask of this row or nullptr */
-    int V;
-    const int *pid;          /* sorted distinct penalised ids */
-    const float *pval;       /* their penalised values (mask applied first) */
-    int np;
-    const uint32_t *pflag;   /* bit per 64-element chunk holding a penalised id */
-    float M, inv_t, maxv;
-    const uint64_t *tab;
-};
-
-DLK_DEV float prepared(const Row &R, int i) {
-    float x = R.lg[i];
-    if (R.mk && !((R.mk[i >> 5] >> (i & 31)) & 1u)) x = -INFINITY;
-    if (R.np && ((R.pflag[i >> 11] >> ((i >> 6) & 31)) & 1u)) {
-        int lo = 0, hi = R.np;
-        while (lo < hi) {
-            int mid = (lo + hi) >> 1;
-            if (R.pid[mid] < i) lo = mid + 1;
-            else hi = mid;
-        }
-        if (lo < R.np && R.pid[lo] == i) x = R.pval[lo];
-    }
-    return x;
-}
-
-DLK_DEV float scaled(const Row &R, int i) { return (prepared(R, i) - R.M) * R.inv_t; }
-DLK_DEV float expo(const Row &R, float s) { return dlk_expf_glibc(s - R.maxv, R.tab); }
-
-/* --------------------------------------------------------------- LDS layout */
-
-struct Lds {
-    uint64_t *tab;      /* 32 */
-    double *red;        /* 64 doubles of reduction scratch */
-    double *bd;         /* 16 doubles: broadcast slots */
-    int *bi;            /* 64 ints: broadcast slots */
-    uint32_t *hsort;    /* hcap: history ids (sort buffer) */
-    int *pid;           /* hcap */
-    float *pval;        /* hcap */
-    int *pcnt;          /* hcap */
-    uint32_t *pflag;    /* flag words */
-    unsigned char *region;
-};
-
-DLK_DEV unsigned char *carve(unsigned char *&p, size_t bytes) {
-    unsigned char *r = p;
-    p += (bytes + 15) & ~(size_t)15;
-    return r;
-}
-
-DLK_DEV Lds make_lds(unsigned char *base, const LdsPlan &pl) {
-    Lds L;
-    unsigned char *p = base;
-    L.tab = (uint64_t *)carve(p, 32 * 8);
-    L.red = (double *)carve(p, 64 * 8);
-    L.bd = (double *)carve(p, 16 * 8);
-    L.bi = (int *)carve(p, 64 * 4);
-    L.hsort = (uint32_t *)carve(p, (size_t)pl.hcap * 4);
-    L.pid = (int *)carve(p, (size_t)pl.hcap * 4);
-    L.pval = (float *)carve(p, (size_t)pl.hcap * 4);
-    L.pcnt = (int *)carve(p, (size_t)pl.hcap * 4);
-    L.pflag = (uint32_t *)carve(p, (size_t)pl.flag_words * 4);
-    L.region = p;
-    return L;
-}
-
-DLK_DEV Aggs make_aggs(unsigned char *p, int n) {
-    const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
-    Aggs A;
-    A.a0 = (uint64_t *)carve(p, (size_t)nch * 8);
-    A.a1 = (uint64_t *)carve(p, (size_t)nch * 8);
-    A.bh = (int *)carve(p, (size_t)nch * 4);
-    A.ga0 = (uint64_t *)carve(p, (size_t)ngr * 8);
-    A.ga1 = (uint64_t *)carve(p, (size_t)ngr * 8);
-    A.gbh = (int *)carve(p, (size_t)ngr * 4);
-    A.P = (double *)carve(p, (size_t)(nch + 1) * 8);
-    return A;
-}
-
-/* ------------------------------------------------------------ block helpers */
-
-/* Bitonic sort (ascending) of n = power of two 64-bit keys in LDS. */
-template <class K>
-__device__ void bitonic_sort(K *a, int n) {
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < n; i += blockDim.x) {
-                int l = i ^ j;
-                if (l > i) {
-                    K x = a[i], y = a[l];
-                    bool up = (i & k) == 0;
-                    if ((x > y) == up) { a[i] = y; a[l] = x; }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-/* Block reduce of (value, index): larger value wins, ties to the lower index;
- * NaN never wins (src/sampler.c:13 compares with '>'). */
-__device__ void block_argmax(float &v, int &i, Lds &L) {
-    const int lane = lane_id(), w = wave_id();
-    for (int m = 32; m >= 1; m >>= 1) {
-        float ov = shfl_xor(v, m);
-        int oi = shfl_xor(i, m);
-        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-    }
-    float *rv = (float *)L.red;
-    int *ri = (int *)(L.red + 32);
-    if (lane == 0) { rv[w] = v; ri[w] = i; }
-    __syncthreads();
-    if (w == 0) {
-        int nw = n_waves();
-        v = lane < nw ? rv[lane] : -INFINITY;
-        i = lane < nw ? ri[lane] : 0x7fffffff;
-        for (int m = 32; m >= 1; m >>= 1) {
-            float ov = shfl_xor(v, m);
-            int oi = shfl_xor(i, m);
-            if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-        }
-        if (lane == 0) { rv[0] = v; ri[0] = i; }
-    }
-    __syncthreads();
-    v = rv[0];
-    i = ri[0];
-    __syncthreads();
-}
-
-__device__ int block_sum_int(int v, Lds &L) {
-    const int lane = lane_id(), w = wave_id();
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-    int *r = (int *)L.red;
-    if (lane == 0) r[w] = v;
-    __syncthreads();
-    int s = 0;
-    for (int k = 0; k < n_waves(); k++) s += r[k];
-    __syncthreads();
-    return s;
-}
-
-/* ----------------------------------------------------- penalties (patches) */
-
-/* Deduplicate the row's history and compute each distinct id's penalised value:
- * the mask first (grammar runs before the penalties, src/core/sampler_api.c:51-61),
- * then the ops in `order`; repetition is applied once per occurrence
- * (src/sampler.c:23-31), presence and frequency once per distinct id. */
-__device__ int build_patches(const RowParams &p, int row, const float *lg, const uint32_t *mk, Lds &L,
-                             const LdsPlan &pl, int V) {
-    const int t = threadIdx.x, T = blockDim.x;
-    int np = 0;
-    for (int w = t; w < pl.flag_words; w += T) L.pflag[w] = 0;
-    if (!p.hist_off) return 0;
-    const int h0 = p.hist_off[row], h1 = p.hist_off[row + 1];
-    const int nh = h1 - h0;
-    if (nh <= 0) { __syncthreads(); return 0; }
-    for (int i = t; i < pl.hcap; i += T) {
-        uint32_t v = 0xffffffffu;
-        if (i < nh) {
-            int id = p.hist_ids[h0 + i];
-            if (id >= 0 && id < V) v = (uint32_t)id;
-        }
-        L.hsort[i] = v;
-    }
-    __syncthreads();
-    bitonic_sort(L.hsort, pl.hcap);
-    /* run lengths at run starts */
-    for (int i = t; i < pl.hcap; i += T) {
-        uint32_t v = L.hsort[i];
-        int c = 0;
-        if (v != 0xffffffffu && (i == 0 || L.hsort[i - 1] != v)) {
-            int j = i;
-            while (j < pl.hcap && L.hsort[j] == v) j++;
-            c = j - i;
-        }
-        L.pcnt[i] = c;
-    }
-    __syncthreads();
-    if (wave_id() == 0) {
-        const int lane = lane_id();
-        int base = 0;
-        for (int i0 = 0; i0 < pl.hcap; i0 += 64) {
-            int i = i0 + lane;
-            int c = L.pcnt[i];
-            uint32_t v = L.hsort[i];
-            uint64_t bal = ballot(c > 0);
-            int at = base + __popcll(bal & ((1ull << lane) - 1));
-            if (c > 0) { L.pid[at] = (int)v; L.pval[at] = (float)c; }
-            base += __popcll(bal);
-        }
-        if (lane == 0) L.bi[0] = base;
-    }
-    __syncthreads();
-    np = L.bi[0];
-    for (int j = t; j < np; j += T) {
-        int id = L.pid[j];
-        int cnt = (int)L.pval[j];
-        float x = lg[id];
-        if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-        for (int s = 0; s < 8; s++) {
-            uint32_t op = (p.order >> (4 * s)) & 0xFu;
-            if (op == 0) break;
-            if (op == DLK_OP_REPETITION) {
-                if (p.rep > 1.0f)
-                    for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
-            } else if (op == DLK_OP_FREQUENCY) {
-                if (p.freq != 0.0f) {
-                    float d = p.freq * (float)cnt;
-                    x = x - d;
-                }
-            } else if (op == DLK_OP_PRESENCE) {
-                if (p.pres != 0.0f) x = x - p.pres;
-            }
-        }
-        L.pval[j] = x;
-        atomicOr(&L.pflag[id >> 11], 1u << ((id >> 6) & 31));
-    }
-    __syncthreads();
-    return np;
-}
-
-/* ------------------------------------------------------------- exact top-k */
-
-/* First k elements under (s desc, index asc), sorted, into cand[0..k) as
- * (desc_key << 32 | index).  Radix select on the 32-bit key (11/11/10 bits),
- * then collection; ties at the k-th key are taken in index order. */
-__device__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32_t *hist, Lds &L) {
-    const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id();
-    uint32_t prefix = 0;
-    int krem = k, below_total = 0, eq_count = 0;
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    for (int rd = 0; rd < 3; rd++) {
-        const int sh = shifts[rd], nb = 1 << widths[rd];
-        const int hsh = rd == 0 ? 32 : shifts[rd - 1];
-        for (int b = t; b < nb; b += T) hist[b] = 0;
-        __syncthreads();
-        for (int i = t; i < V; i += T) {
-            uint32_t key = desc_key(scaled(R, i));
-            bool in = rd == 0 || (key >> hsh) == prefix;
-            if (in) atomicAdd(&hist[(key >> sh) & (nb - 1)], 1u);
-        }
-        __syncthreads();
-        if (wave_id() == 0) {
-            const int per = nb / 64;
-            uint32_t loc = 0;
-            for (int b = 0; b < per; b++) loc += hist[lane * per + b];
-            uint32_t inc = loc;
-            for (int d = 1; d < 64; d <<= 1) {
-                uint32_t o = shfl_up(inc, d);
-                if (lane >= d) inc += o;
-            }
-            uint32_t exc = inc - loc;
-            bool hit = exc < (uint32_t)krem && inc >= (uint32_t)krem;
-            uint64_t bal = ballot(hit);
-            int hl = first_lane(bal);
-            if (lane == hl) {
-                uint32_t run = exc;
-                int b = 0;
-                for (; b < per; b++) {
-                    uint32_t c = hist[lane * per + b];
-                    if (run + c >= (uint32_t)krem) break;
-                    run += c;
-                }
-                L.bi[4] = lane * per + b;
-                L.bi[5] = (int)run;
-                L.bi[6] = (int)hist[lane * per + b];
-            }
-        }
-        __syncthreads();
-        int d = L.bi[4], below = L.bi[5];
-        eq_count = L.bi[6];
-        __syncthreads();
-        prefix = (rd == 0) ? (uint32_t)d : ((prefix << widths[rd]) | (uint32_t)d);
-        krem -= below;
-        below_total += below;
-    }
-    const uint32_t kstar = prefix;
-    const int need = k - below_total;     /* >= 1 elements with key == kstar */
-    int *cnt = L.bi + 8;                  /* [0] appended, [1] ties taken */
-    if (t == 0) { cnt[0] = 0; cnt[1] = 0; }
-    __syncthreads();
-    const bool ordered_ties = eq_count > need;
-    for (int i = t; i < V; i += T) {
-        uint32_t key = desc_key(scaled(R, i));
-        bool take = key < kstar || (!ordered_ties && key == kstar);
-        if (take) {
-            int at = atomicAdd(&cnt[0], 1);
-            cand[at] = ((uint64_t)key << 32) | (uint32_t)i;
-        }
-    }
-    __syncthreads();
-    if (ordered_ties) {
-        /* index-ordered pass over the ties, stopping after `need` of them */
-        int *wcnt = (int *)L.red;
-        for (int i0 = 0; i0 < V; i0 += T) {
-            int taken = cnt[1];
-            if (taken >= need) break;
-            int i = i0 + t;
-            bool tie = i < V && desc_key(scaled(R, i)) == kstar;
-            uint64_t bal = ballot(tie);
-            if (lane == 0) wcnt[wave_id()] = __popcll(bal);
-            __syncthreads();
-            int before = 0;
-            for (int w = 0; w < wave_id(); w++) before += wcnt[w];
-            int rank = taken + before + __popcll(bal & ((1ull << lane) - 1));
-            if (tie && rank < need) cand[below_total + rank] = ((uint64_t)kstar << 32) | (uint32_t)i;
-            __syncthreads();
-            if (t == 0) {
-                int tot = 0;
-                for (int w = 0; w < n_waves(); w++) tot += wcnt[w];
-                cnt[1] = taken + tot;
-            }
-            __syncthreads();
-        }
-    }
-    for (int i = k + t; i < kp; i += T) cand[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort(cand, kp);
-}
-
-/* -------------------------------------------------------- sampling pipeline */
-
-/* Base sequence of the softmax: e_j over candidate positions j < n. */
-struct FullBase {           /* k = V: position j is token j */
-    const Row *R;
-    DLK_DEV float e(int j) const { return expo(*R, scaled(*R, j)); }
-    DLK_DEV int token(int j) const { return j; }
-};
-struct CandBase {           /* top-k: position j is cand[j] */
-    const Row *R;
-    const uint64_t *cand;
-    DLK_DEV float s(int j) const { return key_value((uint32_t)(cand[j] >> 32)); }
-    DLK_DEV float e(int j) const { return expo(*R, s(j)); }
-    DLK_DEV int token(int j) const { return (int)(uint32_t)cand[j]; }
-};
-
-struct Scal {               /* row scalars of the later stages */
-    float inv, inv2, inv3, min_p;
-    int minp_on, minp_all, topp_on, cut;     /* cut: last kept position */
-};
-
-template <class B>
-struct QSoft {              /* p_j = e_j * inv_sum (src/sampler.c:183-185) */
-    const B *b; const Scal *S;
-    DLK_DEV float operator()(int j) const { return b->e(j) * S->inv; }
-};
-template <class B>
-struct QExp {
-    const B *b;
-    DLK_DEV float operator()(int j) const { return b->e(j); }
-};
-template <class B>
-struct QSurv {              /* min-p survivors (src/sampler.c:191-195) */
-    const B *b; const Scal *S;
-    DLK_DEV float operator()(int j) const {
-        float pj = b->e(j) * S->inv;
-        return (S->minp_all || pj >= S->min_p) ? pj : 0.0f;
-    }
-};
-template <class B>
-struct QTopP {              /* input of the top-p cumulation */
-    const B *b; const Scal *S;
-    DLK_DEV float operator()(int j) const {
-        float pj = b->e(j) * S->inv;
-        if (!S->minp_on) return pj;
-        if (!(S->minp_all || pj >= S->min_p)) return 0.0f;
-        return pj * S->inv2;
-    }
-};
-template <class B>
-struct QDraw {              /* final probabilities (src/sampler.c:221, :228) */
-    const B *b; const Scal *S;
-    DLK_DEV float operator()(int j) const {
-        QTopP<B> tp{b, S};
-        float v = tp(j);
-        if (!S->topp_on) return v;
-        return j <= S->cut ? v * S->inv3 : 0.0f;
-    }
-};
-
-/* Runs one exact sum: block builds aggregates, wave 0 resolves, all threads get
- * (pos, value). */
-template <int MB, class QF>
-__device__ ResolveOut<MB> exact_sum(int n, const QF &q, const Aggs &A, double scale, double cut, bool has_thr,
-                                    double thr, Lds &L) {
-    build_aggs<MB>(n, q, A, scale, cut);
-    if (wave_id() == 0) {
-        ResolveOut<MB> o = resolve<MB>(n, q, A, has_thr, thr);
-        if (lane_id() == 0) { L.bi[16] = o.pos; L.bd[8] = (double)o.value; }
-    }
-    __syncthreads();
-    ResolveOut<MB> o;
-    o.pos = L.bi[16];
-    o.value = (typename Fmt<MB>::T)L.bd[8];
-    __syncthreads();
-    return o;
-}
-
-/* The reference's softmax/min-p/top-p/draw over n candidate positions.
- * Returns the sampled position; fills S. */
-template <class B>
-__device__ int pipeline(const RowParams &p, const B &base, int n, float r, unsigned char *region, Lds &L, Scal &S) {
-    Aggs A = make_aggs(region, n);
-    S.inv2 = 1.0f; S.inv3 = 1.0f; S.min_p = p.min_p;
-    S.minp_on = p.minp_on; S.minp_all = 0; S.topp_on = p.topp_on; S.cut = n - 1;
-    /* softmax sum, src/sampler.c:177-182 */
-    QExp<B> qe{&base};
-    chunk_prefix(n, qe, A.P, L.red);
-    ResolveOut<53> s1 = exact_sum<53>(n, qe, A, 1.0, INFINITY, false, 0.0, L);
-    S.inv = (float)(1.0 / s1.value);
-    double scale = S.inv;
-    if (S.minp_on) {
-        /* src/sampler.c:188-202: survivors p >= min_p, all kept if none. */
-        int cnt = 0, last = -1;
-        for (int j = threadIdx.x; j < n; j += blockDim.x) {
-            if (base.e(j) * S.inv >= S.min_p) { cnt++; last = max(last, j); }
-        }
-        cnt = block_sum_int(cnt, L);
-        for (int m = 32; m >= 1; m >>= 1) last = max(last, shfl_xor(last, m));
-        if (lane_id() == 0) L.bi[32 + wave_id()] = last;
-        __syncthreads();
-        int lastall = -1;
-        for (int w = 0; w < n_waves(); w++) lastall = max(lastall, L.bi[32 + w]);
-        __syncthreads();
-        S.minp_all = cnt == 0;
-        S.cut = S.minp_all ? n - 1 : lastall;
-        QSurv<B> qs{&base, &S};
-        chunk_prefix(n, qs, A.P, L.red);
-        ResolveOut<53> s2 = exact_sum<53>(n, qs, A, 1.0, INFINITY, false, 0.0, L);
-        S.inv2 = (float)(1.0 / s2.value);
-        scale = S.inv2;
-    }
-    int last_kept = S.cut;
-    if (S.topp_on) {
-        QTopP<B> qt{&base, &S};
-        double s3;
-        int x;
-        if (p.top_p <= 0.0f) {
-            /* cumul after the first kept entry is that entry: nk = 1 */
-            x = 0;
-            if (S.minp_on && !S.minp_all) {
-                int first = n;
-                for (int j = threadIdx.x; j < n; j += blockDim.x)
-                    if (base.e(j) * S.inv >= S.min_p) first = min(first, j);
-                for (int m = 32; m >= 1; m >>= 1) first = min(first, shfl_xor(first, m));
-                if (lane_id() == 0) L.bi[32 + wave_id()] = first;
-                __syncthreads();
-                x = n;
-                for (int w = 0; w < n_waves(); w++) x = min(x, L.bi[32 + w]);
-                __syncthreads();
-            }
-            s3 = (double)qt(x);
-        } else {
-            ResolveOut<53> o = exact_sum<53>(n, qt, A, scale, INFINITY, true, p.topp_thr, L);
-            x = o.pos >= 0 ? o.pos : last_kept;
-            s3 = o.value;
-        }
-        S.inv3 = (float)(1.0 / s3);
-        S.cut = x;
-        last_kept = x;
-        scale = scale * (double)S.inv3;
-    }
-    /* draw, src/sampler.c:225-233: first j with r < cumul (cumul >= nextafter(r)) */
-    QDraw<B> qd{&base, &S};
-    double cutP = A.P[min((n + 63) >> 6, (last_kept >> 6) + 1)];
-    double vthr = (double)u2f(f2u(r) + 1u);
-    ResolveOut<24> d = exact_sum<24>(n, qd, A, scale, cutP, true, vthr, L);
-    return d.pos >= 0 ? d.pos : last_kept;
-}
 
 /* ------------------------------------------------------------------- kernel */
 

@@ -1,0 +1,38 @@
+/*
+ * sampler_topk.h -- parameters and workspace slots of the single-pass top-k path.
+ */
+#ifndef DLK_SAMPLER_TOPK_H
+#define DLK_SAMPLER_TOPK_H
+
+#include "sampler_params.h"
+
+namespace dlk {
+
+constexpr int kTopkThreads = 512;
+
+/* What each slice workgroup publishes (relaxed agent-scope atomic stores). */
+struct TopkSlot {
+    uint32_t max_bits;   /* slice maximum of the prepared logits */
+    uint32_t argmax;     /* its lowest index */
+    uint32_t nfin;       /* finite entries in the slice */
+    uint32_t kept;       /* candidates published */
+    uint32_t complete;   /* 1: every finite entry published; 0: partial; 0xffffffff: overflow */
+    uint32_t last_key;   /* desc key of the last published candidate */
+    uint32_t first_nan;  /* slice 0 only: prepared logit 0 is NaN (greedy rule) */
+    uint32_t pad;
+};
+
+struct TopkParams {
+    RowParams p;
+    int G;               /* workgroups per row */
+    int S;               /* slice length = EPT * kTopkThreads */
+    int KP;              /* candidates kept per slice: min(k + 16, ...) */
+    int buf_cap;         /* LDS collect / merge buffer entries (power of two) */
+    uint32_t *counters;  /* [rows], zero between launches */
+    TopkSlot *slots;     /* [rows * G] */
+    uint64_t *cands;     /* [rows * G * KP] */
+};
+
+}  // namespace dlk
+
+#endif

@@ -1,0 +1,376 @@
+/*
+ * sampler_topk.hip -- single-pass top-k sampling path (top-k active or greedy).
+ *
+ * One row is split over G workgroups.  Each streams its contiguous slice once
+ * into registers (128-bit loads), applies the allow-mask and the penalty patches
+ * of the ids in its slice, and keeps its local candidates: the first K' = k + 16
+ * elements under (prepared logit desc, index asc).  The last workgroup of the row
+ * to finish (relaxed agent-scope atomics: no cache flushes, no spin waits) merges
+ * the G candidate lists.  Because s = (l - M) * (1/T) is monotone in l but not
+ * injective, the merge re-sorts on s and certifies that no unseen element of any
+ * slice can tie the k-th s; rows it cannot certify (long runs of equal s) rerun
+ * the exact selection over the whole row in the same workgroup.  The merged top-k
+ * then goes through the exact softmax / top-p / draw pipeline.
+ *
+ * Reference: src/sampler.c:109-134 (top-k order), :136-234 (pipeline),
+ * src/sampler.c:9-19 (greedy), src/core/sampler_api.c:51-61 (mask, penalties).
+ */
+#include "sampler_common.h"
+#include "sampler_topk.h"
+
+namespace dlk {
+
+DLK_DEV uint32_t asc_key(float l) {          /* ascending orderable key, -0 == +0 */
+    return ~desc_key(l);
+}
+
+DLK_DEV void pub32(uint32_t *a, uint32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DLK_DEV void pub64(uint64_t *a, uint64_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DLK_DEV uint32_t get32(const uint32_t *a) {
+    return __hip_atomic_load((uint32_t *)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DLK_DEV uint64_t get64(const uint64_t *a) {
+    return __hip_atomic_load((uint64_t *)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Penalised value of token id: mask first, then the ops in order; the
+ * occurrence count is read from the whole history (src/sampler.c:21-52). */
+DLK_DEV float penalised(const RowParams &p, float x, int cnt) {
+    for (int s = 0; s < 8; s++) {
+        uint32_t op = (p.order >> (4 * s)) & 0xFu;
+        if (op == 0) break;
+        if (op == DLK_OP_REPETITION) {
+            if (p.rep > 1.0f)
+                for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
+        } else if (op == DLK_OP_FREQUENCY) {
+            if (p.freq != 0.0f) {
+                float d = p.freq * (float)cnt;
+                x = x - d;
+            }
+        } else if (op == DLK_OP_PRESENCE) {
+            if (p.pres != 0.0f) x = x - p.pres;
+        }
+    }
+    return x;
+}
+
+template <int EPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const RowParams &p = f.p;
+    const int g = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = lane_id(), w = wave_id();
+    const int T = kTopkThreads, V = p.V, G = f.G;
+    const int s0 = g * f.S, s1 = min(V, s0 + f.S);
+    const float *lg = p.logits + (int64_t)row * p.ld;
+    const uint32_t *mk = nullptr;
+    if (p.mask) mk = p.mask + (int64_t)(p.mask_row ? p.mask_row[row] : row) * p.mask_ld;
+
+    /* LDS: the row-kernel layout (for the in-workgroup fallback) + fast-path buffers */
+    Lds L = make_lds(smem, p.plan);
+    unsigned char *q = L.region;
+    uint32_t *sbits = (uint32_t *)carve(q, (size_t)(f.S / 32) * 4);          /* patched positions in slice */
+    float *tmax = (float *)carve(q, (size_t)T * 4);
+    int *misc = (int *)carve(q, 64 * 4);
+    uint64_t *buf = (uint64_t *)carve(q, (size_t)f.buf_cap * 8);           /* collect / merge / fallback */
+    if (t < 32) L.tab[t] = kExp2Tab[t];
+
+    const int32_t *hist = nullptr;
+    int nh = 0;
+    if (p.hist_off) {
+        hist = p.hist_ids + p.hist_off[row];
+        nh = p.hist_off[row + 1] - p.hist_off[row];
+    }
+
+    /* ---- 1. penalty patches of the ids inside this slice ---------------- */
+    for (int i = t; i < f.S / 32; i += T) sbits[i] = 0;
+    if (t == 0) misc[0] = 0;
+    __syncthreads();
+    for (int i = t; i < nh; i += T) {          /* in-slice occurrences, first occurrence only */
+        int id = hist[i];
+        if (id < s0 || id >= s1) continue;
+        bool first = true;
+        int cnt = 0;
+        for (int j = 0; j < nh; j++) {
+            int o = hist[j];
+            if (o == id) { cnt++; if (j < i) first = false; }
+        }
+        if (!first) continue;
+        float x = lg[id];
+        if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+        x = penalised(p, x, cnt);
+        int at = atomicAdd(&misc[0], 1);
+        if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = x; }
+        atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
+    }
+    __syncthreads();
+    const int np = min(misc[0], p.plan.hcap);
+
+    /* ---- 2. stream the slice into registers ---------------------------- */
+    float v[EPT];
+    float tm = -INFINITY;
+    int targ = 0x7fffffff, nfin = 0;
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        float4 x4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (i0 + 3 < s1) {
+            x4 = *(const float4 *)(lg + i0);
+        } else {
+            if (i0 < s1) x4.x = lg[i0];
+            if (i0 + 1 < s1) x4.y = lg[i0 + 1];
+            if (i0 + 2 < s1) x4.z = lg[i0 + 2];
+        }
+        float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+        uint32_t mw = 0xffffffffu;
+        if (mk && i0 < s1) mw = mk[i0 >> 5] >> (i0 & 31);
+        uint32_t pb = 0;
+        if (i0 < s1) pb = (sbits[(i0 - s0) >> 5] >> ((i0 - s0) & 31)) & 0xFu;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int i = i0 + c;
+            float x = xs[c];
+            if (!((mw >> c) & 1u)) x = -INFINITY;
+            if ((pb >> c) & 1u) {
+                for (int k = 0; k < np; k++)
+                    if (L.pid[k] == i) x = L.pval[k];
+            }
+            if (i >= s1) x = -INFINITY;
+            v[j4 * 4 + c] = x;
+            if (i < s1) {
+                if (x > tm || (x == tm && i < targ)) { tm = x; targ = i; }
+                nfin += (x > -INFINITY);
+            }
+        }
+    }
+    /* ---- 3. workgroup max / argmax / finite count ----------------------- */
+    float bm = tm;
+    int bi = targ;
+    block_argmax(bm, bi, L);
+    int nf = block_sum_int(nfin, L);
+    TopkSlot *slot = f.slots + ((int64_t)row * G + g);
+    uint64_t *cands = f.cands + ((int64_t)row * G + g) * f.KP;
+
+    int kept = 0, complete = 1;
+    uint32_t last_key = 0;
+    if (!p.greedy && nf > 0) {
+        /* ---- 4. threshold: the KP-th largest thread maximum ------------- */
+        ((uint32_t *)tmax)[t] = asc_key(tm);
+        __syncthreads();
+        bitonic_sort((uint32_t *)tmax, T);
+        const int KP = f.KP;
+        uint32_t thr_key = ((uint32_t *)tmax)[T - min(KP, T)];   /* KP-th largest thread max */
+        float thr = key_value(~thr_key);
+        if (!(thr > -INFINITY)) thr = -INFINITY;
+        /* ---- 5. collect finite elements >= thr ------------------------- */
+        if (t == 0) misc[1] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPT; j++) {
+            const int i = s0 + 4 * (t + (j / 4) * T) + (j & 3);
+            float x = v[j];
+            bool take = x > -INFINITY && x >= thr;
+            uint64_t bal = ballot(take);
+            int base = 0;
+            if (lane == 0 && bal) base = atomicAdd(&misc[1], __popcll(bal));
+            base = shfl(base, 0);
+            int at = base + __popcll(bal & ((1ull << lane) - 1));
+            if (take && at < f.buf_cap) buf[at] = ((uint64_t)desc_key(x) << 32) | (uint32_t)i;
+        }
+        __syncthreads();
+        const int C = misc[1];
+        if (C > f.buf_cap) {
+            complete = -1;                     /* overflow: the merge falls back */
+        } else {
+            int P = 64;
+            while (P < C) P <<= 1;
+            for (int i = C + t; i < P; i += T) buf[i] = ~0ull;
+            __syncthreads();
+            bitonic_sort(buf, P);
+            kept = min(KP, C);
+            complete = (C == nf) ? 1 : 0;
+            last_key = (uint32_t)(buf[kept - 1] >> 32);
+            for (int j = t; j < kept; j += T) pub64(&cands[j], buf[j]);
+        }
+    }
+    /* ---- 6. publish and elect the merging workgroup --------------------- */
+    if (t == 0) {
+        pub32(&slot->max_bits, f2u(bm));
+        pub32(&slot->argmax, (uint32_t)bi);
+        pub32(&slot->nfin, (uint32_t)nf);
+        pub32(&slot->kept, (uint32_t)kept);
+        pub32(&slot->complete, (uint32_t)complete);
+        pub32(&slot->last_key, last_key);
+        pub32(&slot->first_nan, (g == 0 && isnan(v[0])) ? 1u : 0u);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        uint32_t old = __hip_atomic_fetch_add(&f.counters[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        misc[2] = old == (uint32_t)(G - 1);
+    }
+    __syncthreads();
+    if (!misc[2]) return;
+
+    /* ===================== merge (last workgroup of the row) ============== */
+    if (t == 0) pub32(&f.counters[row], 0u);
+    /* slot h -> LDS (misc[16..]: kept, complete, last_key per slice; up to 64 slices per pass) */
+    uint32_t *sk = (uint32_t *)tmax;                 /* tmax is free now: 3 words per slice */
+    float M = -INFINITY;
+    int amax = 0x7fffffff, NF = 0, total = 0, overflow = 0, first_nan = 0;
+    for (int h = t; h < G; h += T) {
+        TopkSlot *s = f.slots + ((int64_t)row * G + h);
+        sk[3 * h + 0] = get32(&s->kept);
+        sk[3 * h + 1] = get32(&s->complete);
+        sk[3 * h + 2] = get32(&s->last_key);
+        buf[h] = ((uint64_t)get32(&s->max_bits) << 32) | get32(&s->argmax);
+        buf[G + h] = ((uint64_t)get32(&s->nfin) << 32) | get32(&s->first_nan);
+    }
+    __syncthreads();
+    for (int h = 0; h < G; h++) {           /* identical in every thread, slice order */
+        float m = u2f((uint32_t)(buf[h] >> 32));
+        int a = (int)(uint32_t)buf[h];
+        if (m > M || (m == M && a < amax)) { M = m; amax = a; }
+        NF += (int)(buf[G + h] >> 32);
+        first_nan |= (int)(uint32_t)buf[G + h];
+        total += (int)sk[3 * h];
+        overflow |= (int)sk[3 * h + 1] == -1;
+    }
+    __syncthreads();
+    const int n_out = p.n_out;
+    auto out_cands_empty = [&](float pr, float lpv, bool ids_idx, int kk) {
+        for (int j = t; j < n_out; j += T) {
+            int64_t o = (int64_t)row * n_out + j;
+            if (p.out_cand_ids) p.out_cand_ids[o] = ids_idx ? (j < kk ? j : -1) : -1;
+            if (p.out_cand_probs) p.out_cand_probs[o] = pr;
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = lpv;
+        }
+    };
+    if (p.greedy) {
+        if (t == 0) p.out_ids[row] = (first_nan || amax == 0x7fffffff) ? 0 : amax;
+        out_cands_empty(0.0f, -INFINITY, false, 0);
+        return;
+    }
+    uint64_t st = xorshift64(p.rng[row]);
+    const float r = rand_f32_from(st);
+    __syncthreads();
+    if (t == 0) p.rng[row] = st;
+    const int k = p.top_k;
+    if (NF == 0) {                           /* every entry -inf (see sampler_row.hip) */
+        if (t == 0) p.out_ids[row] = k - 1;
+        out_cands_empty(NAN, NAN, true, k);
+        return;
+    }
+
+    Row R;
+    R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = 0; R.pflag = L.pflag;
+    R.M = M; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab;
+
+    /* gather candidates re-keyed on s, sorted (s desc, index asc) */
+    bool ok = !overflow && total <= f.buf_cap;
+    int P = 64;
+    if (ok) {
+        while (P < total) P <<= 1;
+        int at = 0;
+        for (int h = 0; h < G; h++) {
+            int kh = (int)sk[3 * h];
+            const uint64_t *ch = f.cands + ((int64_t)row * G + h) * f.KP;
+            for (int j = t; j < kh; j += T) {
+                uint64_t c = get64(&ch[j]);
+                float l = key_value((uint32_t)(c >> 32));
+                float s_ = (l - M) * R.inv_t;
+                buf[at + j] = ((uint64_t)desc_key(s_) << 32) | (c & 0xffffffffull);
+            }
+            at += kh;
+        }
+        for (int i = total + t; i < P; i += T) buf[i] = ~0ull;
+        __syncthreads();
+        bitonic_sort(buf, P);
+        if (NF >= k) {
+            /* certify: every slice that kept only part of its finite elements
+             * must have its last kept candidate strictly below the k-th s */
+            uint32_t kth = (uint32_t)(buf[k - 1] >> 32);
+            for (int h = 0; h < G; h++) {
+                if ((int)sk[3 * h + 1] == 1) continue;
+                float l = key_value(sk[3 * h + 2]);
+                if (!(desc_key((l - M) * R.inv_t) > kth)) ok = false;
+            }
+        } else {
+            /* fewer finite entries than k: all of them plus the first k-NF
+             * entries that are -inf, in index order */
+            if (total != NF) ok = false;
+        }
+    }
+    __syncthreads();
+    if (!ok) {
+        /* exact selection over the whole row in this workgroup */
+        int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
+        R.np = np_row;
+        uint32_t *hist2 = (uint32_t *)(buf + p.plan.kp);
+        select_top_k(R, k, buf, p.plan.kp, hist2, L);
+    } else if (NF < k) {
+        /* append the first k-NF -inf entries in index order */
+        int need = k - NF, found = 0;
+        int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
+        R.np = np_row;
+        for (int i0 = 0; i0 < V && found < need; i0 += T) {
+            int i = i0 + t;
+            bool ninf = i < V && !(prepared(R, i) > -INFINITY);
+            uint64_t bal = ballot(ninf);
+            if (lane == 0) misc[8 + w] = __popcll(bal);
+            __syncthreads();
+            int before = 0, tot = 0;
+            for (int u = 0; u < n_waves(); u++) { if (u < w) before += misc[8 + u]; tot += misc[8 + u]; }
+            int rank = found + before + __popcll(bal & ((1ull << lane) - 1));
+            if (ninf && rank < need) buf[NF + rank] = ((uint64_t)desc_key(-INFINITY) << 32) | (uint32_t)i;
+            __syncthreads();
+            found += tot;
+        }
+        __syncthreads();
+    }
+    CandBase cb{&R, buf};
+    R.maxv = cb.s(0);
+    Scal S;
+    unsigned char *reg = (unsigned char *)(buf + f.buf_cap);
+    int pos = pipeline(p, cb, k, r, reg, L, S);
+    if (t == 0) p.out_ids[row] = cb.token(pos);
+    for (int j = t; j < n_out; j += T) {
+        int64_t o = (int64_t)row * n_out + j;
+        if (j < k) {
+            float pj = cb.e(j) * S.inv;
+            QDraw<CandBase> qd{&cb, &S};
+            float fj = qd(j);
+            if (p.out_cand_ids) p.out_cand_ids[o] = cb.token(j);
+            if (p.out_cand_probs) p.out_cand_probs[o] = pj;
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
+        } else {
+            if (p.out_cand_ids) p.out_cand_ids[o] = -1;
+            if (p.out_cand_probs) p.out_cand_probs[o] = 0.0f;
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = -INFINITY;
+        }
+    }
+}
+
+}  // namespace dlk
+
+extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
+    using namespace dlk;
+    static int set[5] = {0, 0, 0, 0, 0};
+    const void *fns[5] = {(const void *)topk_kernel<4>, (const void *)topk_kernel<8>, (const void *)topk_kernel<16>,
+                          (const void *)topk_kernel<32>, (const void *)topk_kernel<64>};
+    int which = ept == 4 ? 0 : ept == 8 ? 1 : ept == 16 ? 2 : ept == 32 ? 3 : ept == 64 ? 4 : -1;
+    if (which < 0) return -1;
+    if (!set[which]) {
+        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return -1;
+        set[which] = 1;
+    }
+    dim3 grid(f->G, rows);
+    switch (which) {
+        case 0: hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(kTopkThreads), lds, stream, *f); break;
+        case 1: hipLaunchKernelGGL(topk_kernel<8>, grid, dim3(kTopkThreads), lds, stream, *f); break;
+        case 2: hipLaunchKernelGGL(topk_kernel<16>, grid, dim3(kTopkThreads), lds, stream, *f); break;
+        case 3: hipLaunchKernelGGL(topk_kernel<32>, grid, dim3(kTopkThreads), lds, stream, *f); break;
+        default: hipLaunchKernelGGL(topk_kernel<64>, grid, dim3(kTopkThreads), lds, stream, *f); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -55,7 +55,11 @@ typedef struct {
     uint32_t penalty_order;   /* DLK_ORDER_* or any packing of DLK_OP_* */
     int max_history;          /* upper bound on any row's history length (LDS sizing) */
     int n_out;                /* candidate outputs per row (0 = none) */
+    int path;                 /* DLK_PATH_AUTO, or DLK_PATH_ROW to force the one-workgroup-per-row kernel */
 } dlk_sample_params;
+
+#define DLK_PATH_AUTO 0
+#define DLK_PATH_ROW 1
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */

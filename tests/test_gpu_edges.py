@@ -1,0 +1,138 @@
+"""GPU parity on edge cases, through both paths of dlk_sample (automatic dispatch
+and the forced one-workgroup-per-row kernel): greedy, masked rows, fewer finite
+entries than k, long runs of equal logits at the k-th value, min-p, top-p <= 0 /
+= 1, tiny vocabularies, out-of-range and repeated history ids.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from diskllm_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+PATHS = [0, 1]   # automatic dispatch, forced row kernel
+
+
+def make(name, rows, V, seed=0, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, rep=1.0, freq=0.0, pres=0.0,
+         order=W.ORDER_REFERENCE, hist=None, mask=None, logits=None, n_out=0):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    lg = logits if logits is not None else rng.normal(0, 3, size=(rows, V)).astype(np.float32)
+    hoff = hids = None
+    if hist is not None:
+        hoff = np.zeros(rows + 1, np.int32)
+        hoff[1:] = np.cumsum([len(h) for h in hist])
+        hids = np.concatenate([np.asarray(h, np.int32) for h in hist]).astype(np.int32)
+    seeds = rng.integers(1, 2 ** 63, size=rows, dtype=np.uint64)
+    return W.Workload(name, rows, V, np.ascontiguousarray(lg, np.float32), seeds, temperature=temperature,
+                      top_k=top_k, top_p=top_p, min_p=min_p, repeat_penalty=rep, frequency_penalty=freq,
+                      presence_penalty=pres, order=order, hist_off=hoff, hist_ids=hids, mask=mask, n_out=n_out)
+
+
+def run_and_check(w, path):
+    from diskllm_amd import api
+    print(f"[case] {w.name} rows={w.rows} V={w.vocab} k={w.top_k} p={w.top_p} minp={w.min_p} T={w.temperature} "
+          f"path={path}", flush=True)
+    db = api.to_device(w)
+    api.sample(db, api.params_of(w, path=path))
+    res = api.results(db)
+    for r in range(w.rows):
+        o = O.sample_row(O.prepared_row(w, r), int(w.seeds[r]), w.temperature, w.top_k, w.top_p, w.min_p,
+                         want_p=w.n_out)
+        assert int(res["ids"][r]) == o["token"], (w.name, r, int(res["ids"][r]), o["token"])
+        assert int(res["states"][r]) == o["state"], (w.name, r)
+        if w.n_out and o["k"] and not o["greedy"] and np.all(np.isfinite(o["cand_p"])):
+            n = min(w.n_out, o["k"])
+            np.testing.assert_array_equal(res["cand_ids"][r, :n], o["cand_idx"][:n])
+            np.testing.assert_allclose(res["cand_probs"][r, :n], o["cand_p"][:n], rtol=1e-5)
+    assert res["status"] == 0
+    return res
+
+
+def mask_rows(rows, V, allowed_lists):
+    m = np.zeros((rows, (V + 31) // 32), np.uint32)
+    for r, al in enumerate(allowed_lists):
+        al = np.asarray(al, np.int64)
+        if al.size:
+            np.bitwise_or.at(m[r], al >> 5, (np.uint32(1) << (al & 31).astype(np.uint32)))
+    return m
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_greedy(cuda, path):
+    w = make("greedy", 6, 50000, seed=1, temperature=0.0, top_k=40, hist=[[1, 2, 3]] * 6, rep=1.3)
+    w.logits[2, 777] = w.logits[2].max() + 1
+    w.logits[2, 9000] = w.logits[2, 777]          # tie: lowest index wins
+    w.logits[3, :] = -np.inf                      # all -inf: index 0
+    w.logits[4, 0] = np.nan                       # NaN at 0: index 0 (src/sampler.c:11-17)
+    res = run_and_check(w, path)
+    assert res["ids"][2] == 777 and res["ids"][3] == 0 and res["ids"][4] == 0
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_masked_rows_topk(cuda, path):
+    V = 40000
+    rng = np.random.default_rng(5)
+    allowed = [[], [1234], list(rng.choice(V, 7, replace=False)), list(rng.choice(V, 300, replace=False)),
+               list(range(V - 5, V)), [0]]
+    w = make("masked", len(allowed), V, seed=2, temperature=0.7, top_k=20, top_p=0.9,
+             mask=mask_rows(len(allowed), V, allowed), n_out=24)
+    res = run_and_check(w, path)
+    assert res["ids"][0] == 19                    # all masked: candidate k-1 in index order
+    assert res["ids"][1] == 1234 and res["ids"][5] == 0
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_masked_rows_full_vocab(cuda, path):
+    V = 30000
+    allowed = [[], [4321], list(range(0, V, 97))]
+    w = make("masked-full", 3, V, seed=3, temperature=1.0, top_p=0.95, mask=mask_rows(3, V, allowed))
+    res = run_and_check(w, path)
+    assert res["ids"][0] == V - 1 and res["ids"][1] == 4321
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_ties_at_kth(cuda, path):
+    V = 70000
+    rows = 4
+    lg = np.random.default_rng(7).normal(0, 1, size=(rows, V)).astype(np.float32)
+    lg[0, :] = 1.5                                # every entry equal: first k by index
+    lg[1, ::3] = 4.0                              # 23k-way tie above the rest
+    lg[2, 10:5000] = 9.0                          # contiguous tie block
+    lg[3, :] = np.round(lg[3] * 4) / 4            # quantised logits: many s ties
+    w = make("ties", rows, V, seed=4, temperature=0.9, top_k=50, top_p=0.8, logits=lg, n_out=50)
+    res = run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_min_p_and_top_p_edges(cuda, path):
+    V = 20000
+    for tp, mp, k in [(0.0, 0.0, 30), (-1.0, 0.0, 0), (1.0, 0.0, 30), (0.5, 0.02, 0), (0.9, 0.001, 64),
+                      (0.9, 0.9, 16), (1.0, 0.05, 0)]:
+        w = make(f"edges-p{tp}-minp{mp}-k{k}", 5, V, seed=11, temperature=0.6, top_k=k, top_p=tp, min_p=mp)
+        w.logits[:, 17] += 12.0                   # one dominant token
+        run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_tiny_vocab_and_history(cuda, path):
+    for V in (1, 2, 3, 63, 64, 65, 4095, 4097):
+        hist = [[0, 0, V - 1, V + 5, -3, 1, 1, 1], [], [V // 2] * 40]
+        w = make(f"tiny{V}", 3, V, seed=V, temperature=1.3, top_k=min(5, V), top_p=0.97, rep=1.2, pres=0.4,
+                 freq=0.1, order=W.ORDER_NORTH_STAR, hist=hist)
+        run_and_check(w, path)
+        w2 = make(f"tiny{V}-full", 3, V, seed=V + 1, temperature=0.5, top_p=0.9, rep=1.5, hist=hist)
+        run_and_check(w2, path)
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_penalty_orders(cuda, path):
+    V = 50000
+    rng = np.random.default_rng(9)
+    hist = [list(rng.integers(0, 50, 200)), list(rng.integers(0, V, 300))]
+    for order in (W.ORDER_REFERENCE, W.ORDER_NORTH_STAR, W.pack_order(W.OP_FREQUENCY, W.OP_PRESENCE,
+                                                                        W.OP_REPETITION)):
+        w = make(f"order{order:x}", 2, V, seed=12, temperature=1.0, top_k=100, top_p=0.95, rep=1.3, freq=0.2,
+                 pres=-0.7, order=order, hist=hist)
+        w.logits[:, :50] = np.linspace(-6, 6, 50, dtype=np.float32)
+        run_and_check(w, path)

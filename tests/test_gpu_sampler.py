@@ -18,10 +18,10 @@ def _announce(msg):
     print(f"[case] {msg}", flush=True)
 
 
-def run_gpu(w, rows=None):
+def run_gpu(w, rows=None, path=0):
     from diskllm_amd import api
     db = api.to_device(w, rows=rows)
-    api.sample(db)
+    api.sample(db, api.params_of(w, path=path))
     return api.results(db)
 
 
@@ -100,10 +100,11 @@ def test_device_expf_exhaustive(cuda):
     assert bad_total == 0
 
 
-def test_c1_single_row(cuda):
+@pytest.mark.parametrize("path", [0, 1])
+def test_c1_single_row(cuda, path):
     w = W.c1()
-    _announce(f"C1 V={w.vocab}")
-    res = run_gpu(w)
+    _announce(f"C1 V={w.vocab} path={path}")
+    res = run_gpu(w, path=path)
     assert_rows_match(w, res, [0])
 
 
@@ -122,10 +123,11 @@ def test_c2_reference_order(cuda):
     assert_rows_match(w, res, list(range(w.rows)))
 
 
-def test_c3_packed_mask(cuda):
+@pytest.mark.parametrize("path", [0, 1])
+def test_c3_packed_mask(cuda, path):
     w = W.c3()
-    _announce(f"C3 rows={w.rows} V={w.vocab}")
-    res = run_gpu(w)
+    _announce(f"C3 rows={w.rows} V={w.vocab} path={path}")
+    res = run_gpu(w, path=path)
     orc = assert_rows_match(w, res, list(range(w.rows)))
     # row 3 allows exactly one token: it must be returned
     allowed = np.nonzero(np.unpackbits(w.mask[3].view(np.uint8), bitorder="little")[:w.vocab])[0]
@@ -143,8 +145,9 @@ def test_c4_dfa_masks(cuda):
         np.testing.assert_array_equal(got[r], ref, err_msg=f"row {r} state {w.dfa_states[r]}")
 
 
-def test_c5_gemma_dfa_topk(cuda):
+@pytest.mark.parametrize("path", [0, 1])
+def test_c5_gemma_dfa_topk(cuda, path):
     w = W.c5()
-    _announce(f"C5 rows={w.rows} V={w.vocab}")
-    res = run_gpu(w)
+    _announce(f"C5 rows={w.rows} V={w.vocab} path={path}")
+    res = run_gpu(w, path=path)
     assert_rows_match(w, res, list(range(w.rows)))
