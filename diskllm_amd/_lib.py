@@ -19,7 +19,7 @@ DLK_ERR_INVALID = -1
 DLK_ERR_UNSUPPORTED = -2
 DLK_ERR_HIP = -3
 DLK_STATUS_HISTORY_TOO_LONG = 1
-PATH_AUTO, PATH_ROW = 0, 1
+PATH_AUTO, PATH_ROW, PATH_FULL_EXACT = 0, 1, 2
 
 OP_REPETITION, OP_FREQUENCY, OP_PRESENCE = 1, 2, 3
 ORDER_REFERENCE = OP_PRESENCE | (OP_REPETITION << 4)

@@ -12,9 +12,12 @@
 
 #include "sampler_params.h"
 #include "sampler_topk.h"
+#include "sampler_full.h"
 
 extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t lds_bytes, hipStream_t stream);
 extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream);
+extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds);
 
 namespace {
 
@@ -134,6 +137,68 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     return dlk_launch_topk_kernel(&f, rows, ept, lds, stream) == 0 ? DLK_OK : DLK_ERR_HIP;
 }
 
+/* Fused full-vocabulary path (sampler_full.hip): DLK_OK, or 1 when outside its
+ * range (the caller then uses the row kernel). */
+int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStream_t stream) {
+    using namespace dlk;
+    const int T = kFullThreads;
+    if (p.greedy || p.topk_on || p.minp_on) return 1;
+    if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
+    if (vocab < 8192) return 1;
+    int G = (256 + rows - 1) / rows;
+    if (G > kFullMaxG) G = kFullMaxG;
+    if (G < 1) G = 1;
+    int ept = (vocab + G * T - 1) / (G * T);
+    ept = ept <= 32 ? 32 : ept <= 48 ? 48 : ept <= 64 ? 64 : ept <= 80 ? 80 : 96;
+    G = (vocab + ept * T - 1) / (ept * T);
+    if (G > kFullMaxG) return 1;
+    const int S = ept * T;
+    if (p.n_out > S) return 1;
+    const int nch = S / 64, ngr = (nch + 63) / 64;
+    FullParams f;
+    memset(&f, 0, sizeof(f));
+    f.G = G;
+    f.S = S;
+    f.stage_cap = 64;
+    f.force_exact = force_exact;
+    size_t lds = fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
+                 2 * r16((size_t)nch * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)ngr * 8) + r16((size_t)ngr * 4) +
+                 r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) +
+                 r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
+    if (lds > kMaxLds) return 1;
+    int cap = dlk_full_kernel_capacity(ept, lds);
+    int rows_per = cap / G;
+    if (rows_per < 1) return 1;
+    if (rows_per > rows) rows_per = rows;
+    const size_t fb_bytes = r16(aggs_bytes(vocab));
+    const size_t n_pub = r16((size_t)rows_per * G * kPubWords * 8);
+    const size_t n_cv = r16((size_t)rows_per * G * kCandSlots * 64 * 4);
+    WsView ws;
+    if (!workspace((size_t)rows_per * kSyncWords, n_pub + n_cv + (size_t)rows_per * fb_bytes, ws)) return DLK_ERR_HIP;
+    f.sync = ws.counters;
+    f.pub = (uint64_t *)ws.data;
+    f.cvals = (float *)(ws.data + n_pub);
+    f.fb = ws.data + n_pub + n_cv;
+    f.fb_bytes = fb_bytes;
+    for (int r0 = 0; r0 < rows; r0 += rows_per) {
+        const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;
+        f.p = p;
+        f.p.logits = p.logits + (int64_t)r0 * p.ld;
+        if (p.hist_off) f.p.hist_off = p.hist_off + r0;
+        if (p.mask) {
+            if (p.mask_row) f.p.mask_row = p.mask_row + r0;
+            else f.p.mask = p.mask + (int64_t)r0 * p.mask_ld;
+        }
+        f.p.rng = p.rng + r0;
+        f.p.out_ids = p.out_ids + r0;
+        if (p.out_cand_ids) f.p.out_cand_ids = p.out_cand_ids + (int64_t)r0 * p.n_out;
+        if (p.out_cand_probs) f.p.out_cand_probs = p.out_cand_probs + (int64_t)r0 * p.n_out;
+        if (p.out_cand_logprobs) f.p.out_cand_logprobs = p.out_cand_logprobs + (int64_t)r0 * p.n_out;
+        if (dlk_launch_full_kernel(&f, nr, ept, lds, stream) != 0) return DLK_ERR_HIP;
+    }
+    return DLK_OK;
+}
+
 }  // namespace
 
 extern "C" uint64_t dlk_seed_state(uint64_t seed) { return seed ? seed : 0xDEADBEEF12345678ULL; }
@@ -183,6 +248,10 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
     size_t total = fixed + region;
     if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on)) {
         int rc = launch_topk(p, rows, vocab, stream);
+        if (rc <= 0) return rc;
+    }
+    if ((prm->path == DLK_PATH_AUTO || prm->path == DLK_PATH_FULL_EXACT) && !p.greedy && !p.topk_on) {
+        int rc = launch_full(p, rows, vocab, prm->path == DLK_PATH_FULL_EXACT, stream);
         if (rc <= 0) return rc;
     }
     if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;

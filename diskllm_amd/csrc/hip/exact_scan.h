@@ -176,7 +176,7 @@ struct Aggs {
 /* Block-wide: P[c] = approximate exclusive prefix of q over chunks, P[nch] = total.
  * Uses `red` (>= blockDim/64 doubles of LDS) as scratch. */
 template <class QF>
-__device__ void chunk_prefix(int n, const QF &q, double *P, double *red) {
+__device__ __forceinline__ void chunk_prefix(int n, const QF &q, double *P, double *red) {
     const int lane = lane_id(), w = wave_id(), nw = n_waves();
     const int nch = (n + 63) >> 6;
     for (int c = w; c < nch; c += nw) {
@@ -212,7 +212,7 @@ __device__ void chunk_prefix(int n, const QF &q, double *P, double *red) {
 /* Block-wide: chunk and group aggregates of q under binades predicted from
  * scale * min(P, cut). */
 template <int MB, class QF>
-__device__ void build_aggs(int n, const QF &q, const Aggs &A, double scale, double cut) {
+__device__ __forceinline__ void build_aggs(int n, const QF &q, const Aggs &A, double scale, double cut) {
     const int lane = lane_id(), w = wave_id(), nw = n_waves();
     const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
     for (int c = w; c < nch; c += nw) {
@@ -251,16 +251,19 @@ struct ResolveOut {
     typename Fmt<MB>::T value;      /* running value after `pos` (or after the last element) */
 };
 
-/* One wave: walk the sequence with the aggregates.  has_thr selects a stop at
- * the first element after which c >= thr_v.  All lanes return the same result. */
+/* One wave: walk the sequence with the aggregates, starting from the running
+ * value c0.  has_thr selects a stop at the first element after which c >= thr_v.
+ * All lanes return the same result. */
 template <int MB, class QF>
-__device__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs &A, bool has_thr, double thr_v) {
+__device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs &A, bool has_thr, double thr_v,
+                                  typename Fmt<MB>::T c0 = 0) {
     using T = typename Fmt<MB>::T;
     const int lane = lane_id();
     const uint64_t top = 1ull << MB;
     const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
-    int b = Fmt<MB>::EMIN;
-    uint64_t m = 0;
+    int b;
+    uint64_t m;
+    split(c0, b, m);
     uint64_t thr = has_thr ? ceil_div_pow2(thr_v, b - (MB - 1)) : kCap;
     int pos = 0, cap = 2;
     while (pos < n) {

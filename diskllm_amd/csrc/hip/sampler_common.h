@@ -113,7 +113,7 @@ DLK_DEV Aggs make_aggs(unsigned char *p, int n) {
 
 /* Bitonic sort (ascending) of n = power of two 64-bit keys in LDS. */
 template <class K>
-__device__ void bitonic_sort(K *a, int n) {
+__device__ __forceinline__ void bitonic_sort(K *a, int n) {
     for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
             for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -131,7 +131,7 @@ __device__ void bitonic_sort(K *a, int n) {
 
 /* Block reduce of (value, index): larger value wins, ties to the lower index;
  * NaN never wins (src/sampler.c:13 compares with '>'). */
-__device__ void block_argmax(float &v, int &i, Lds &L) {
+__device__ __forceinline__ void block_argmax(float &v, int &i, Lds &L) {
     const int lane = lane_id(), w = wave_id();
     for (int m = 32; m >= 1; m >>= 1) {
         float ov = shfl_xor(v, m);
@@ -159,7 +159,7 @@ __device__ void block_argmax(float &v, int &i, Lds &L) {
     __syncthreads();
 }
 
-__device__ int block_sum_int(int v, Lds &L) {
+__device__ __forceinline__ int block_sum_int(int v, Lds &L) {
     const int lane = lane_id(), w = wave_id();
     for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
     int *r = (int *)L.red;
@@ -177,7 +177,7 @@ __device__ int block_sum_int(int v, Lds &L) {
  * the mask first (grammar runs before the penalties, src/core/sampler_api.c:51-61),
  * then the ops in `order`; repetition is applied once per occurrence
  * (src/sampler.c:23-31), presence and frequency once per distinct id. */
-__device__ int build_patches(const RowParams &p, int row, const float *lg, const uint32_t *mk, Lds &L,
+__device__ __forceinline__ int build_patches(const RowParams &p, int row, const float *lg, const uint32_t *mk, Lds &L,
                              const LdsPlan &pl, int V) {
     const int t = threadIdx.x, T = blockDim.x;
     int np = 0;
@@ -256,15 +256,15 @@ __device__ int build_patches(const RowParams &p, int row, const float *lg, const
 /* First k elements under (s desc, index asc), sorted, into cand[0..k) as
  * (desc_key << 32 | index).  Radix select on the 32-bit key (11/11/10 bits),
  * then collection; ties at the k-th key are taken in index order. */
-__device__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32_t *hist, Lds &L) {
+__device__ __forceinline__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32_t *hist, Lds &L) {
     const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id();
     uint32_t prefix = 0;
     int krem = k, below_total = 0, eq_count = 0;
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
     for (int rd = 0; rd < 3; rd++) {
-        const int sh = shifts[rd], nb = 1 << widths[rd];
-        const int hsh = rd == 0 ? 32 : shifts[rd - 1];
+        const int sh = rd == 0 ? 21 : rd == 1 ? 10 : 0;
+        const int width = rd == 2 ? 10 : 11;
+        const int nb = 1 << width;
+        const int hsh = rd == 0 ? 32 : rd == 1 ? 21 : 10;
         for (int b = t; b < nb; b += T) hist[b] = 0;
         __syncthreads();
         for (int i = t; i < V; i += T) {
@@ -303,7 +303,7 @@ __device__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32
         int d = L.bi[4], below = L.bi[5];
         eq_count = L.bi[6];
         __syncthreads();
-        prefix = (rd == 0) ? (uint32_t)d : ((prefix << widths[rd]) | (uint32_t)d);
+        prefix = (rd == 0) ? (uint32_t)d : ((prefix << width) | (uint32_t)d);
         krem -= below;
         below_total += below;
     }
@@ -414,7 +414,7 @@ struct QDraw {              /* final probabilities (src/sampler.c:221, :228) */
 /* Runs one exact sum: block builds aggregates, wave 0 resolves, all threads get
  * (pos, value). */
 template <int MB, class QF>
-__device__ ResolveOut<MB> exact_sum(int n, const QF &q, const Aggs &A, double scale, double cut, bool has_thr,
+__device__ __forceinline__ ResolveOut<MB> exact_sum(int n, const QF &q, const Aggs &A, double scale, double cut, bool has_thr,
                                     double thr, Lds &L) {
     build_aggs<MB>(n, q, A, scale, cut);
     if (wave_id() == 0) {
@@ -432,7 +432,7 @@ __device__ ResolveOut<MB> exact_sum(int n, const QF &q, const Aggs &A, double sc
 /* The reference's softmax/min-p/top-p/draw over n candidate positions.
  * Returns the sampled position; fills S. */
 template <class B>
-__device__ int pipeline(const RowParams &p, const B &base, int n, float r, unsigned char *region, Lds &L, Scal &S) {
+__device__ __forceinline__ int pipeline(const RowParams &p, const B &base, int n, float r, unsigned char *region, Lds &L, Scal &S) {
     Aggs A = make_aggs(region, n);
     S.inv2 = 1.0f; S.inv3 = 1.0f; S.min_p = p.min_p;
     S.minp_on = p.minp_on; S.minp_all = 0; S.topp_on = p.topp_on; S.cut = n - 1;

@@ -1,0 +1,54 @@
+/*
+ * sampler_full.h -- parameters of the fused full-vocabulary path (top-k off).
+ */
+#ifndef DLK_SAMPLER_FULL_H
+#define DLK_SAMPLER_FULL_H
+
+#include "sampler_params.h"
+
+namespace dlk {
+
+constexpr int kFullThreads = 512;
+constexpr int kFullMaxG = 16;        /* workgroups per row */
+constexpr int kPubWords = 16;        /* 64-bit words each workgroup publishes */
+constexpr int kCandSlots = 2;        /* predicted top-p crossing chunks per workgroup */
+constexpr int kSyncWords = 64;       /* per-row synchronisation words */
+
+/* per-row sync words (all zero between launches) */
+enum : int {
+    kSyncA = 0,        /* row maximum published */
+    kSyncB = 1,        /* softmax partial sums published */
+    kSyncC = 2,        /* top-p partial sums + crossing chunks published */
+    kSyncExit = 3,     /* workgroups finished */
+    kSyncDone = 4,     /* token written */
+    kSyncChain = 16,   /* + w: running value for workgroup w is ready */
+    kSyncChainVal = 32 /* + w: that running value (float bits) */
+};
+
+/* published words per workgroup */
+enum : int {
+    kPubMax = 0,       /* float bits of the slice maximum */
+    kPubE = 1,         /* double: slice sum of e */
+    kPubP = 2,         /* double: slice sum of p */
+    kPubNCand = 3,     /* number of crossing-candidate chunks */
+    kPubCandChunk = 4, /* + s: global chunk index */
+    kPubCandPre = 6,   /* + s: double, slice-local exclusive p prefix at that chunk */
+    kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
+};
+
+struct FullParams {
+    RowParams p;
+    int G;             /* workgroups per row */
+    int S;             /* slice length = EPT * kFullThreads */
+    int stage_cap;     /* chunks of final probabilities kept in LDS per workgroup */
+    uint32_t *sync;    /* [rows][kSyncWords] */
+    uint64_t *pub;     /* [rows][G][kPubWords] */
+    float *cvals;      /* [rows][G][kCandSlots][64] */
+    unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
+    size_t fb_bytes;
+    int force_exact;   /* test hook: send every row through the exact fallback */
+};
+
+}  // namespace dlk
+
+#endif

@@ -1,0 +1,640 @@
+/*
+ * sampler_full.hip -- fused full-vocabulary sampling (top-k off, min-p off):
+ * src/sampler.c:136-234 with k = V, bit-exact, one HBM pass.
+ *
+ * A row is split over G workgroups (cooperative launch, so all of a row's
+ * workgroups are resident); each keeps its slice in registers.  The row is
+ * tied together by three row barriers and a chain, all through relaxed
+ * agent-scope atomics (every shared word is an atomic store/load; each writer
+ * waits for its stores before it signals, so no cache-flushing fences are needed):
+ *
+ *   A  slice maxima            -> M (src/sampler.c:155-158)
+ *   B  slice sums of e         -> inv = (float)(1/sum), certified: the sequential
+ *                                 double sum (:177-181) lies within a proven
+ *                                 relative bound of our sum, and inv is taken only
+ *                                 if every value in that interval gives the same
+ *                                 float (:182)
+ *   C  slice sums of p and the few chunks that can hold the top-p crossing
+ *                              -> every workgroup computes the same certified cut x
+ *                                 and inv3 (:207-220)
+ *   chain  each workgroup walks its slice with the exact float running sum of the
+ *          draw (:226-232, exact_scan.h), starting from its predecessor's exact
+ *          value, and hands its end value on; the one that crosses r writes the
+ *          token.
+ *
+ * Rows whose sums cannot be certified (the bound straddles a float rounding
+ * boundary; probability ~1e-3 per row) are finished by workgroup 0 alone with the
+ * exact sequential emulation of every sum (the general pipeline).
+ */
+#include "sampler_common.h"
+#include "sampler_full.h"
+
+namespace dlk {
+
+constexpr uint32_t kSpinLimit = 1u << 24;
+
+DLK_DEV void at_st32(uint32_t *a, uint32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DLK_DEV void at_st64(uint64_t *a, uint64_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DLK_DEV uint32_t at_ld32(const uint32_t *a) {
+    return __hip_atomic_load((uint32_t *)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DLK_DEV uint64_t at_ld64(const uint64_t *a) {
+    return __hip_atomic_load((uint64_t *)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* All G workgroups of the row arrive; returns when all have (bounded wait). */
+__device__ __forceinline__ void row_barrier(uint32_t *ctr, int G, uint32_t *status) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t spins = 0;
+        while (at_ld32(ctr) < (uint32_t)G) {
+            if (++spins > kSpinLimit) {
+                if (status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+/* Last workgroup of the row to leave returns the row's sync words to zero. */
+__device__ __forceinline__ void row_exit(uint32_t *sync, int G) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t old = __hip_atomic_fetch_add(&sync[kSyncExit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (uint32_t)(G - 1))
+            for (int i = 0; i < kSyncWords; i++) at_st32(&sync[i], 0u);
+    }
+}
+
+/* Exclusive scan of P[0..n) in place, P[n] = total (deterministic order). */
+__device__ __forceinline__ void block_excl_scan(double *P, int n, double *red) {
+    const int lane = lane_id(), w = wave_id(), T = blockDim.x, t = threadIdx.x;
+    const int per = (n + T - 1) / T;
+    const int b0 = t * per, b1 = min(n, b0 + per);
+    double loc = 0.0;
+    for (int c = b0; c < b1; c++) loc += P[c];
+    double inc = loc;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        double o = shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    double wbase = 0.0;
+    for (int k = 0; k < w; k++) wbase += red[k];
+    double run = wbase + inc - loc;
+    __syncthreads();
+    for (int c = b0; c < b1; c++) { double v = P[c]; P[c] = run; run += v; }
+    if (t == T - 1) P[n] = run;
+    __syncthreads();
+}
+
+/* Element values of the draw inside one slice: staged chunks from LDS, anything
+ * else recomputed from the logits exactly as the registers held it. */
+struct QSlice {
+    const int *smap;
+    const float *svals;
+    const float *lg;
+    const uint32_t *mk;
+    const uint32_t *sbits;
+    const int *pid;
+    const float *pval;
+    int np, s0, x, topp;
+    float M, inv_t, inv, inv3;
+    const uint64_t *tab;
+    DLK_DEV float operator()(int i) const {
+        int sl = smap[i >> 6];
+        if (sl >= 0) return svals[sl * 64 + (i & 63)];
+        const int gi = s0 + i;
+        if (gi > x) return 0.0f;
+        float l = lg[gi];
+        if (mk && !((mk[gi >> 5] >> (gi & 31)) & 1u)) l = -INFINITY;
+        if ((sbits[i >> 5] >> (i & 31)) & 1u)
+            for (int k = 0; k < np; k++)
+                if (pid[k] == gi) l = pval[k];
+        float e = dlk_expf_glibc((l - M) * inv_t, tab);
+        float pj = e * inv;
+        return topp ? pj * inv3 : pj;
+    }
+};
+
+template <int EPT>
+__global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const RowParams &p = f.p;
+    const int G = f.G, T = kFullThreads;
+    const int row = blockIdx.x / G, g = blockIdx.x % G;
+    const int t = threadIdx.x, lane = lane_id();
+    const int V = p.V, S = f.S, nch = S / 64, ngr = (nch + 63) / 64;
+    const int s0 = g * S, s1 = min(V, s0 + S);
+    const float *lg = p.logits + (int64_t)row * p.ld;
+    const uint32_t *mk = nullptr;
+    if (p.mask) mk = p.mask + (int64_t)(p.mask_row ? p.mask_row[row] : row) * p.mask_ld;
+    uint32_t *sync = f.sync + (int64_t)row * kSyncWords;
+    uint64_t *pubrow = f.pub + (int64_t)row * G * kPubWords;
+    uint64_t *mypub = pubrow + (int64_t)g * kPubWords;
+    float *mycv = f.cvals + ((int64_t)row * G + g) * kCandSlots * 64;
+
+    Lds L = make_lds(smem, p.plan);
+    unsigned char *q = L.region;
+    uint32_t *sbits = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
+    double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);
+    double *cp = (double *)carve(q, (size_t)(nch + 1) * 8);
+    Aggs A;
+    A.a0 = (uint64_t *)carve(q, (size_t)nch * 8);
+    A.a1 = (uint64_t *)carve(q, (size_t)nch * 8);
+    A.bh = (int *)carve(q, (size_t)nch * 4);
+    A.ga0 = (uint64_t *)carve(q, (size_t)ngr * 8);
+    A.ga1 = (uint64_t *)carve(q, (size_t)ngr * 8);
+    A.gbh = (int *)carve(q, (size_t)ngr * 4);
+    A.P = (double *)carve(q, (size_t)(nch + 1) * 8);
+    int *smap = (int *)carve(q, (size_t)nch * 4);
+    float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
+    uint64_t *pc = (uint64_t *)carve(q, (size_t)G * kPubWords * 8);   /* published words, cached */
+    int *misc = (int *)carve(q, 64 * 4);
+    double *md = (double *)carve(q, 16 * 8);
+    if (t < 32) L.tab[t] = kExp2Tab[t];
+
+    const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
+    const float r = rand_f32_from(st);
+
+    /* ---- penalty patches of the ids inside this slice ------------------- */
+    const int32_t *hist = nullptr;
+    int nh = 0;
+    if (p.hist_off) {
+        hist = p.hist_ids + p.hist_off[row];
+        nh = p.hist_off[row + 1] - p.hist_off[row];
+    }
+    if (nh > p.plan.hcap) {
+        if (g == 0 && t == 0) {
+            p.out_ids[row] = -1;
+            if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
+        }
+        row_exit(sync, G);
+        return;
+    }
+    for (int i = t; i < S / 32; i += T) sbits[i] = 0;
+    if (t == 0) misc[0] = 0;
+    __syncthreads();
+    for (int i = t; i < nh; i += T) {
+        int id = hist[i];
+        if (id < s0 || id >= s1) continue;
+        bool first = true;
+        int cnt = 0;
+        for (int j = 0; j < nh; j++) {
+            int o = hist[j];
+            if (o == id) { cnt++; if (j < i) first = false; }
+        }
+        if (!first) continue;
+        float x = lg[id];
+        if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+        for (int s = 0; s < 8; s++) {
+            uint32_t op = (p.order >> (4 * s)) & 0xFu;
+            if (op == 0) break;
+            if (op == DLK_OP_REPETITION) {
+                if (p.rep > 1.0f)
+                    for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
+            } else if (op == DLK_OP_FREQUENCY) {
+                if (p.freq != 0.0f) { float d = p.freq * (float)cnt; x = x - d; }
+            } else if (op == DLK_OP_PRESENCE) {
+                if (p.pres != 0.0f) x = x - p.pres;
+            }
+        }
+        int at = atomicAdd(&misc[0], 1);
+        if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = x; }
+        atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
+    }
+    __syncthreads();
+    const int np = min(misc[0], p.plan.hcap);
+
+    /* ---- stream the slice into registers -------------------------------- */
+    float v[EPT];
+    float tm = -INFINITY;
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        float4 x4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (i0 + 3 < s1) {
+            x4 = *(const float4 *)(lg + i0);
+        } else {
+            if (i0 < s1) x4.x = lg[i0];
+            if (i0 + 1 < s1) x4.y = lg[i0 + 1];
+            if (i0 + 2 < s1) x4.z = lg[i0 + 2];
+        }
+        float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+        uint32_t mw = 0xffffffffu;
+        if (mk && i0 < s1) mw = mk[i0 >> 5] >> (i0 & 31);
+        uint32_t pb = 0;
+        if (i0 < s1) pb = (sbits[(i0 - s0) >> 5] >> ((i0 - s0) & 31)) & 0xFu;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int i = i0 + c;
+            float x = xs[c];
+            if (!((mw >> c) & 1u)) x = -INFINITY;
+            if ((pb >> c) & 1u)
+                for (int k = 0; k < np; k++)
+                    if (L.pid[k] == i) x = L.pval[k];
+            if (i >= s1) x = -INFINITY;
+            v[j4 * 4 + c] = x;
+            tm = fmaxf(tm, x);
+        }
+    }
+
+    /* ---- A: row maximum -------------------------------------------------- */
+    {
+        int dummy = 0;
+        block_argmax(tm, dummy, L);
+    }
+    if (t == 0) at_st64(&mypub[kPubMax], f2u(tm));
+    row_barrier(&sync[kSyncA], G, p.status);
+    if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubMax]);
+    __syncthreads();
+    float M = -INFINITY;
+    for (int h = 0; h < G; h++) M = fmaxf(M, u2f((uint32_t)pc[h]));
+    if (g == 0 && t == 0) p.rng[row] = st;                  /* every workgroup has read it */
+    const int n_out = p.n_out;
+    if (!(M > -INFINITY)) {
+        /* every entry -inf: NaN softmax, the draw falls through to index V-1 */
+        if (g == 0) {
+            if (t == 0) p.out_ids[row] = V - 1;
+            for (int j = t; j < n_out; j += T) {
+                int64_t o = (int64_t)row * n_out + j;
+                if (p.out_cand_ids) p.out_cand_ids[o] = j < V ? j : -1;
+                if (p.out_cand_probs) p.out_cand_probs[o] = NAN;
+                if (p.out_cand_logprobs) p.out_cand_logprobs[o] = NAN;
+            }
+        }
+        row_exit(sync, G);
+        return;
+    }
+
+    /* ---- e and its slice sums ------------------------------------------- */
+    const float inv_t = p.inv_temp;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) v[j] = dlk_expf_glibc((v[j] - M) * inv_t, L.tab);
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
+        for (int m = 1; m < 16; m <<= 1) d += shfl_xor(d, m);
+        if ((lane & 15) == 0) ce[(t + j4 * T) >> 4] = d;
+    }
+    __syncthreads();
+    block_excl_scan(ce, nch, L.red);                        /* ce[c]: e prefix at chunk c; ce[nch]: slice sum */
+    if (t == 0) at_st64(&mypub[kPubE], d2u(ce[nch]));
+
+    /* ---- B: softmax normaliser ------------------------------------------ */
+    row_barrier(&sync[kSyncB], G, p.status);
+    if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubE]);
+    __syncthreads();
+    double Sapx = 0.0, EPw = 0.0;
+    for (int h = 0; h < G; h++) {
+        double e = u2d(pc[h]);
+        if (h < g) EPw += e;
+        Sapx += e;
+    }
+    /* |sequential - exact| <= V u sum; |ours - exact| <= 64 u sum (summation depth) */
+    const double U = 0x1p-53;
+    const double eps_s = ((double)V + 64.0) * U * 1.01 + 4.0 * U;
+    const float inv_a = (float)(1.0 / (Sapx * (1.0 + eps_s)));
+    const float inv_b = (float)(1.0 / (Sapx * (1.0 - eps_s)));
+    bool ok = inv_a == inv_b && !f.force_exact;
+    const float inv = inv_a;
+
+    float inv3 = 1.0f;
+    int x = V - 1;
+    const bool topp = p.topp_on;
+    if (ok) {
+        /* ---- p, its sums, and the chunks that may hold the top-p crossing ---- */
+#pragma unroll
+        for (int j = 0; j < EPT; j++) v[j] = v[j] * inv;
+        if (g == 0) {
+#pragma unroll
+            for (int j = 0; j < EPT; j++) {
+                const int i = 4 * (t + (j / 4) * T) + (j & 3);
+                if (i < n_out && i < V) {
+                    int64_t o = (int64_t)row * n_out + i;
+                    if (p.out_cand_ids) p.out_cand_ids[o] = i;
+                    if (p.out_cand_probs) p.out_cand_probs[o] = v[j];
+                }
+            }
+        }
+#pragma unroll
+        for (int j4 = 0; j4 < EPT / 4; j4++) {
+            double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
+            for (int m = 1; m < 16; m <<= 1) d += shfl_xor(d, m);
+            if ((lane & 15) == 0) cp[(t + j4 * T) >> 4] = d;
+        }
+        __syncthreads();
+        block_excl_scan(cp, nch, L.red);
+        if (t == 0) {
+            at_st64(&mypub[kPubP], d2u(cp[nch]));
+            if (g == 0) at_st64(&mypub[kPubP0], f2u(v[0]));
+            misc[1] = 0;
+        }
+        __syncthreads();
+        const double tau = p.topp_thr;
+        if (topp && p.top_p > 0.0f) {
+            /* p-prefix predicted from the e-prefix: |p - e*inv| <= 2^-24 p each */
+            const double dl = 0x1p-21;
+            for (int c = t; c < nch; c += T) {
+                if (s0 + 64 * c >= s1) continue;
+                double lo = (double)inv * (EPw + ce[c]) * (1.0 - dl);
+                double hi = (double)inv * (EPw + ce[c + 1]) * (1.0 + dl);
+                if (lo <= tau && tau <= hi) {
+                    int s = atomicAdd(&misc[1], 1);
+                    if (s < kCandSlots) misc[2 + s] = c;
+                }
+            }
+            __syncthreads();
+            int ncand = misc[1];
+            if (ncand > kCandSlots) {
+                if (t == 0) at_st64(&mypub[kPubNCand], 0xffffull);
+            } else {
+                if (ncand == 2 && misc[2] > misc[3] && t == 0) { int tmp = misc[2]; misc[2] = misc[3]; misc[3] = tmp; }
+                __syncthreads();
+                for (int s = 0; s < ncand; s++) {
+                    const int c = misc[2 + s];
+#pragma unroll
+                    for (int j4 = 0; j4 < EPT / 4; j4++) {
+                        const int u = t + j4 * T;                 /* 4-element group index */
+                        if ((u >> 4) == c)
+                            for (int k = 0; k < 4; k++)
+                                at_st32((uint32_t *)&mycv[s * 64 + (u & 15) * 4 + k], f2u(v[4 * j4 + k]));
+                    }
+                    if (t == 0) {
+                        at_st64(&mypub[kPubCandChunk + s], (uint64_t)(s0 / 64 + c));
+                        at_st64(&mypub[kPubCandPre + s], d2u(cp[c]));
+                    }
+                }
+                if (t == 0) at_st64(&mypub[kPubNCand], (uint64_t)ncand);
+            }
+        }
+
+        /* ---- C: top-p cut and its normaliser ------------------------------ */
+        row_barrier(&sync[kSyncC], G, p.status);
+        if (t < G * kPubWords) pc[t] = at_ld64(&pubrow[t]);
+        __syncthreads();
+        if (t == 0) {
+            int okc = 1, xx = V - 1;
+            float i3 = 1.0f;
+            if (!topp) {
+                /* no renormalisation (src/sampler.c:205) */
+            } else if (p.top_p <= 0.0f) {
+                xx = 0;                                      /* cumul after the first entry */
+                i3 = (float)(1.0 / (double)u2f((uint32_t)pc[kPubP0]));
+            } else {
+                double RW = 0.0, s3 = 0.0, eps3 = 0.0;
+                bool found = false;
+                for (int h = 0; h < G && okc && !found; h++) {
+                    uint64_t nc = pc[h * kPubWords + kPubNCand];
+                    if (nc == 0xffffull) { okc = 0; break; }
+                    for (int s = 0; s < (int)nc && okc && !found; s++) {
+                        int cg = (int)pc[h * kPubWords + kPubCandChunk + s];
+                        double R = RW + u2d(pc[h * kPubWords + kPubCandPre + s]);
+                        const float *vals = f.cvals + ((int64_t)row * G + h) * kCandSlots * 64 + s * 64;
+                        for (int k = 0; k < 64; k++) {
+                            int i = cg * 64 + k;
+                            if (i >= V) break;
+                            R += (double)u2f(at_ld32((const uint32_t *)&vals[k]));
+                            double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
+                            if (R * (1.0 + e) >= tau) {
+                                if (R * (1.0 - e) >= tau) { found = true; xx = i; s3 = R; eps3 = e; }
+                                else okc = 0;
+                                break;
+                            }
+                        }
+                    }
+                    RW += u2d(pc[h * kPubWords + kPubP]);
+                }
+                if (okc && !found) {
+                    double e = ((double)V + 256.0) * U * 1.01 + 4.0 * U;
+                    if (RW * (1.0 + e) < tau) { xx = V - 1; s3 = RW; eps3 = e; }
+                    else okc = 0;
+                }
+                if (okc) {
+                    float a = (float)(1.0 / (s3 * (1.0 + eps3)));
+                    float b = (float)(1.0 / (s3 * (1.0 - eps3)));
+                    if (a == b) i3 = a;
+                    else okc = 0;
+                }
+            }
+            misc[8] = okc; misc[9] = xx; md[0] = (double)i3;
+        }
+        __syncthreads();
+        ok = misc[8] != 0;
+        x = misc[9];
+        inv3 = (float)md[0];
+        __syncthreads();
+    }
+
+    if (!ok) {
+        /* ---- exact fallback: workgroup 0 runs every sum sequentially-exact -- */
+        if (g == 0) {
+            int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
+            Row R;
+            R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np_row; R.pflag = L.pflag;
+            R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab;
+            FullBase fb{&R};
+            Scal Sc;
+            int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
+            if (t == 0) p.out_ids[row] = pos;
+            for (int j = t; j < n_out; j += T) {
+                int64_t o = (int64_t)row * n_out + j;
+                float pj = fb.e(j) * Sc.inv;
+                QDraw<FullBase> qd{&fb, &Sc};
+                float fj = qd(j);
+                if (p.out_cand_ids) p.out_cand_ids[o] = j;
+                if (p.out_cand_probs) p.out_cand_probs[o] = pj;
+                if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
+            }
+        }
+        row_exit(sync, G);
+        return;
+    }
+
+    /* ---- final probabilities, draw aggregates, staged chunks -------------- */
+    double RWg = 0.0;
+    for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int i = s0 + 4 * (t + (j / 4) * T) + (j & 3);
+        v[j] = i <= x ? (topp ? v[j] * inv3 : v[j]) : 0.0f;
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < EPT; j++) {
+            const int i = 4 * (t + (j / 4) * T) + (j & 3);
+            if (i < n_out && i < V && p.out_cand_logprobs)
+                p.out_cand_logprobs[(int64_t)row * n_out + i] = v[j] > 0.0f ? (float)log((double)v[j]) : -INFINITY;
+        }
+    }
+    /* predicted running value at chunk starts (the p prefix, cut at x, scaled) */
+    const double scale = topp ? (double)inv3 : 1.0;
+    double Rx;
+    {
+        /* p prefix at x: bounded by the prefix at the end of x's chunk */
+        int cx = (x - s0) >> 6;
+        Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + cp[min(nch, cx + 1)]);
+    }
+    for (int c = t; c <= nch; c += T) A.P[c] = fmin(RWg + cp[c], Rx) * scale;
+    __syncthreads();
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int u = t + j4 * T;
+        const int c = u >> 4;
+        int bh = predict_binade<24>(A.P[c]);
+        bool valid = bh == predict_binade<24>(A.P[c + 1]) && bh >= -100;
+        uint32_t sum = 0;
+        bool tie = false;
+        if (valid) {
+            for (int k = 0; k < 4; k++) {
+                float xs = ldexpf(v[4 * j4 + k], 23 - bh);
+                uint32_t n = xs >= 0x1p25f ? (1u << 25) : (uint32_t)rintf(xs);
+                tie |= xs < 0x1p24f && (xs - floorf(xs)) == 0.5f;
+                sum += n;
+            }
+        }
+        for (int m = 1; m < 16; m <<= 1) {
+            sum += shfl_xor(sum, m);
+            tie |= shfl_xor((int)tie, m) != 0;
+        }
+        if ((lane & 15) == 0) {
+            A.a0[c] = sum;
+            A.a1[c] = sum;
+            A.bh[c] = (valid && !tie) ? bh : kInvalidBinade;
+        }
+    }
+    if (t == 0) misc[10] = 0;
+    __syncthreads();
+    {
+        const int wv = wave_id();
+        for (int gr = wv; gr < ngr; gr += n_waves()) {
+            int c = gr * 64 + lane;
+            bool in = c < nch;
+            int b0 = A.bh[gr * 64];
+            bool same = !in || A.bh[c] == b0;
+            bool gok = (ballot(!same) == 0) && b0 != kInvalidBinade;
+            uint64_t sv = in ? A.a0[c] : 0;
+            for (int m = 32; m >= 1; m >>= 1) sv += shfl_xor(sv, m);
+            if (lane == 0) {
+                A.ga0[gr] = sv;
+                A.ga1[gr] = sv;
+                A.gbh[gr] = gok ? b0 : kInvalidBinade;
+            }
+        }
+    }
+    /* chunks the walk may have to open: mispredicted or near a binade edge,
+     * near the draw threshold, holding x, or holding a tie */
+    const double vthr = (double)u2f(f2u(r) + 1u);
+    const double mu = 0x1p-8;
+    for (int c = t; c < nch; c += T) {
+        double a = A.P[c], b = A.P[c + 1];
+        bool want = A.bh[c] == kInvalidBinade ||
+                    predict_binade<24>(a * (1.0 - mu)) != predict_binade<24>(b * (1.0 + mu)) ||
+                    (a * (1.0 - mu) <= vthr && vthr <= b * (1.0 + mu)) ||
+                    (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
+        int sl = -1;
+        if (want && s0 + 64 * c < s1) {
+            sl = atomicAdd(&misc[10], 1);
+            if (sl >= f.stage_cap) sl = -1;
+        }
+        smap[c] = sl;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int u = t + j4 * T;
+        const int sl = smap[u >> 4];
+        if (sl >= 0)
+            for (int k = 0; k < 4; k++) svals[sl * 64 + (u & 15) * 4 + k] = v[4 * j4 + k];
+    }
+    __syncthreads();
+
+    /* ---- chain: exact draw over this slice from the predecessor's value --- */
+    float c_in = 0.0f;
+    if (g > 0) {
+        if (t == 0) {
+            int state = 0;
+            uint32_t spins = 0;
+            while (true) {
+                if (at_ld32(&sync[kSyncDone])) { state = 2; break; }
+                if (at_ld32(&sync[kSyncChain + g])) { state = 1; break; }
+                if (++spins > kSpinLimit) {
+                    if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
+                    state = 2;
+                    break;
+                }
+            }
+            misc[11] = state;
+            if (state == 1) misc[12] = (int)at_ld32(&sync[kSyncChainVal + g]);
+        }
+        __syncthreads();
+        if (misc[11] != 1) {
+            row_exit(sync, G);
+            return;
+        }
+        c_in = u2f((uint32_t)misc[12]);
+    }
+    const int n_loc = min(s1, x + 1) - s0;
+    QSlice qs{smap, svals, lg, mk, sbits, L.pid, L.pval, np, s0, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
+    if (wave_id() == 0) {
+        ResolveOut<24> o = resolve<24>(n_loc, qs, A, true, vthr, c_in);
+        if (lane == 0) { misc[13] = o.pos; misc[14] = (int)f2u(o.value); }
+    }
+    __syncthreads();
+    const int pos = misc[13];
+    int token = -1;
+    if (pos >= 0) token = s0 + pos;
+    else if (x < s1) token = x;              /* nothing crossed r up to x: the last kept entry */
+    if (t == 0) {
+        if (token >= 0) {
+            p.out_ids[row] = token;
+            __builtin_amdgcn_s_waitcnt(0);
+            at_st32(&sync[kSyncDone], 1u);
+        } else {
+            at_st32(&sync[kSyncChainVal + g + 1], (uint32_t)misc[14]);
+            __builtin_amdgcn_s_waitcnt(0);
+            at_st32(&sync[kSyncChain + g + 1], 1u);
+        }
+    }
+    row_exit(sync, G);
+}
+
+}  // namespace dlk
+
+extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
+    using namespace dlk;
+    const void *fns[5] = {(const void *)full_kernel<32>, (const void *)full_kernel<48>, (const void *)full_kernel<64>,
+                          (const void *)full_kernel<80>, (const void *)full_kernel<96>};
+    static int set[5] = {0, 0, 0, 0, 0};
+    int which = ept == 32 ? 0 : ept == 48 ? 1 : ept == 64 ? 2 : ept == 80 ? 3 : ept == 96 ? 4 : -1;
+    if (which < 0) return -1;
+    if (!set[which]) {
+        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return -1;
+        set[which] = 1;
+    }
+    FullParams fp = *f;
+    void *args[] = {&fp};
+    hipError_t e = hipLaunchCooperativeKernel(fns[which], dim3(rows * f->G), dim3(kFullThreads), args, (unsigned)lds,
+                                              stream);
+    return e == hipSuccess ? 0 : -1;
+}
+
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds) {
+    using namespace dlk;
+    const void *fn = ept == 32 ? (const void *)full_kernel<32> : ept == 48 ? (const void *)full_kernel<48>
+                   : ept == 64 ? (const void *)full_kernel<64> : ept == 80 ? (const void *)full_kernel<80>
+                               : (const void *)full_kernel<96>;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return 0;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kFullThreads, lds) != hipSuccess) return 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return per_cu * cus;
+}

@@ -81,6 +81,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
 
+    if (nh > p.plan.hcap) {
+        if (g == 0 && t == 0) {
+            p.out_ids[row] = -1;
+            if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
+        }
+        return;
+    }
     /* ---- 1. penalty patches of the ids inside this slice ---------------- */
     for (int i = t; i < f.S / 32; i += T) sbits[i] = 0;
     if (t == 0) misc[0] = 0;

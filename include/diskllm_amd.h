@@ -31,7 +31,8 @@ extern "C" {
 #define DLK_ERR_HIP (-3)          /* a HIP runtime call failed */
 
 /* Device status bits written by the kernels (dlk_batch.status). */
-#define DLK_STATUS_HISTORY_TOO_LONG 1u
+#define DLK_STATUS_HISTORY_TOO_LONG 1u  /* a row's history exceeded max_history: its id is -1 */
+#define DLK_STATUS_SYNC_TIMEOUT 2u      /* a cross-workgroup wait gave up (results of the call invalid) */
 
 /* Penalty ops, packed low nibble first into dlk_sample_params.penalty_order. */
 #define DLK_OP_REPETITION 1u  /* src/sampler.c:21-33, once per occurrence */
@@ -55,11 +56,12 @@ typedef struct {
     uint32_t penalty_order;   /* DLK_ORDER_* or any packing of DLK_OP_* */
     int max_history;          /* upper bound on any row's history length (LDS sizing) */
     int n_out;                /* candidate outputs per row (0 = none) */
-    int path;                 /* DLK_PATH_AUTO, or DLK_PATH_ROW to force the one-workgroup-per-row kernel */
+    int path;                 /* DLK_PATH_AUTO; the others force one implementation (tests) */
 } dlk_sample_params;
 
-#define DLK_PATH_AUTO 0
-#define DLK_PATH_ROW 1
+#define DLK_PATH_AUTO 0        /* fastest path that covers the configuration */
+#define DLK_PATH_ROW 1         /* one workgroup per row, every sum emulated exactly */
+#define DLK_PATH_FULL_EXACT 2  /* fused full-vocabulary kernel with every row finished by its exact fallback */
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */

@@ -136,3 +136,30 @@ def test_penalty_orders(cuda, path):
                  pres=-0.7, order=order, hist=hist)
         w.logits[:, :50] = np.linspace(-6, 6, 50, dtype=np.float32)
         run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", [0, 1, 2])
+def test_full_vocab_variants(cuda, path):
+    """Full-vocabulary sampling at Qwen vocab through the fused kernel (0), the
+    row kernel (1) and the fused kernel's exact fallback (2)."""
+    V = 151936
+    rng = np.random.default_rng(21)
+    for (T, tp, sd) in [(1.0, 0.9, 31), (0.7, 0.95, 32), (1.3, 1.0, 33), (0.5, 0.0, 34), (2.0, 0.5, 35)]:
+        w = W.c2(seed=sd, rows=8, vocab=V)
+        w.temperature, w.top_p = T, tp
+        w.n_out = 16
+        run_and_check(w, path)
+    w = W.c2(seed=36, rows=6, vocab=V)
+    m = np.zeros((6, (V + 31) // 32), np.uint32)
+    for r in range(6):
+        al = rng.choice(V, [1, 5, 1000, 20000, 100000, V][r], replace=False)
+        np.bitwise_or.at(m[r], al >> 5, (np.uint32(1) << (al & 31).astype(np.uint32)))
+    w.mask = m
+    run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", [0, 2])
+def test_full_vocab_many_rows(cuda, path):
+    """More rows than one cooperative launch holds: the host splits the batch."""
+    w = W.c2(seed=41, rows=300, vocab=16384)
+    run_and_check(w, path)
