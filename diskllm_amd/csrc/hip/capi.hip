@@ -149,7 +149,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     if (G > kFullMaxG) G = kFullMaxG;
     if (G < 1) G = 1;
     int ept = (vocab + G * T - 1) / (G * T);
-    ept = ept <= 32 ? 32 : ept <= 48 ? 48 : ept <= 64 ? 64 : ept <= 80 ? 80 : 96;
+    ept = ept <= 16 ? 16 : ept <= 24 ? 24 : ept <= 32 ? 32 : ept <= 40 ? 40 : 48;
     G = (vocab + ept * T - 1) / (ept * T);
     if (G > kFullMaxG) return 1;
     const int S = ept * T;
@@ -159,7 +159,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     memset(&f, 0, sizeof(f));
     f.G = G;
     f.S = S;
-    f.stage_cap = 64;
+    f.stage_cap = 160;
     f.force_exact = force_exact;
     size_t lds = fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
                  2 * r16((size_t)nch * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)ngr * 8) + r16((size_t)ngr * 4) +

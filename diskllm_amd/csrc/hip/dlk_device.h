@@ -70,6 +70,45 @@ DLK_DEV uint64_t xorshift64(uint64_t x) {
 }
 DLK_DEV float rand_f32_from(uint64_t x) { return u53_to_f32_rn(x >> 11) * (1.0f / 9007199254740992.0f); }
 
+/* DPP controls (gfx9 encoding). */
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+/* Inclusive prefix sum within each 16-lane row (lane 15 holds the row total). */
+DLK_DEV uint32_t row_scan_u32(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr1, 0xf, 0xf, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr2, 0xf, 0xf, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr4, 0xf, 0xf, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr8, 0xf, 0xf, true);
+    return x;
+}
+template <int CTRL>
+DLK_DEV double dpp_row_d(double v) {
+    uint64_t u = (uint64_t)__double_as_longlong(v);
+    int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, true);
+    int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, true);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+/* Inclusive prefix sum of doubles within each 16-lane row. */
+DLK_DEV double row_scan_d(double x) {
+    x += dpp_row_d<kDppRowShr1>(x);
+    x += dpp_row_d<kDppRowShr2>(x);
+    x += dpp_row_d<kDppRowShr4>(x);
+    x += dpp_row_d<kDppRowShr8>(x);
+    return x;
+}
+/* Inclusive wave prefix with saturation at `cap` (values <= cap). */
+DLK_DEV uint32_t wave_scan_sat_u32(uint32_t x, uint32_t cap) {
+    uint32_t t;
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr1, 0xf, 0xf, true); x = min(x + t, cap);
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr2, 0xf, 0xf, true); x = min(x + t, cap);
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr4, 0xf, 0xf, true); x = min(x + t, cap);
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr8, 0xf, 0xf, true); x = min(x + t, cap);
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowBcast15, 0xa, 0xf, false); x = min(x + t, cap);
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowBcast31, 0xc, 0xf, false); x = min(x + t, cap);
+    return x;
+}
+
 /* Wave-wide sum (any order) of a double. */
 DLK_DEV double wave_sum(double v) {
     for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);

@@ -251,12 +251,31 @@ struct ResolveOut {
     typename Fmt<MB>::T value;      /* running value after `pos` (or after the last element) */
 };
 
+DLK_DEV uint64_t readlane64(uint64_t v, int l) {
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+DLK_DEV float readlanef(float v, int l) { return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(v), l)); }
+
+/* Inclusive scan of the lanes' increments, added to m: the running significand
+ * after each lane's element/aggregate (saturating; exact below 2^MB). */
+template <int MB>
+DLK_DEV uint64_t scan_from(uint64_t m, Pair x, int lane) {
+    if (MB == 24 && ballot(x.a0 != x.a1) == 0) {
+        const uint32_t cap32 = 1u << 30;
+        return m + wave_scan_sat_u32((uint32_t)min(x.a0, (uint64_t)cap32), cap32);
+    }
+    x = wave_incl_scan(x, lane);
+    return sat_add(m, (m & 1) ? x.a1 : x.a0);
+}
+
 /* One wave: walk the sequence with the aggregates, starting from the running
  * value c0.  has_thr selects a stop at the first element after which c >= thr_v.
  * All lanes return the same result. */
 template <int MB, class QF>
 __device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs &A, bool has_thr, double thr_v,
-                                  typename Fmt<MB>::T c0 = 0) {
+                                                  typename Fmt<MB>::T c0 = 0) {
     using T = typename Fmt<MB>::T;
     const int lane = lane_id();
     const uint64_t top = 1ull << MB;
@@ -270,19 +289,42 @@ __device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs
         int L = 0;
         if (cap >= 2 && (pos & 4095) == 0) L = 2;
         else if (cap >= 1 && (pos & 63) == 0) L = 1;
-        int item = pos >> (6 * L), count;
-        if (L == 2) count = min(64, ngr - item);
-        else if (L == 1) count = min(64 - (item & 63), nch - item);
-        else count = min(64 - (pos & 63), n - pos);
+        if (L == 0) {
+            /* single elements up to the end of the chunk; each exit from the
+             * binade is one real addition and a re-scan of the remaining lanes */
+            const int count = min(64 - (pos & 63), n - pos);
+            const bool act = lane < count;
+            const float qv = act ? q(pos + lane) : 0.0f;
+            int from = 0;
+            while (true) {
+                Pair x = (act && lane >= from) ? increment(qv, b - (MB - 1)) : Pair{0, 0};
+                uint64_t ma = scan_from<MB>(m, x, lane);
+                bool ev = act && lane >= from && (ma >= top || ma >= thr);
+                int f = first_lane(ballot(ev));
+                if (f >= count) {
+                    if (count > from) m = readlane64(ma, count - 1);
+                    break;
+                }
+                if (f > from) m = readlane64(ma, f - 1);
+                const uint64_t maf = readlane64(ma, f);
+                if (maf < top) return ResolveOut<MB>{pos + f, join<MB>(b, maf)};
+                T c = join<MB>(b, m) + (T)readlanef(qv, f);
+                if (has_thr && (double)c >= thr_v) return ResolveOut<MB>{pos + f, c};
+                split(c, b, m);
+                thr = has_thr ? ceil_div_pow2(thr_v, b - (MB - 1)) : kCap;
+                from = f + 1;
+            }
+            pos += count;
+            cap = 2;
+            continue;
+        }
+        const int item = pos >> (6 * L);
+        const int count = L == 2 ? min(64, ngr - item) : min(64 - (item & 63), nch - item);
         const bool act = lane < count;
         Pair x{0, 0};
         bool valid = true;
-        float qv = 0.0f;
         if (act) {
-            if (L == 0) {
-                qv = q(pos + lane);
-                x = increment(qv, b - (MB - 1));
-            } else if (L == 1) {
+            if (L == 1) {
                 int c = item + lane;
                 valid = A.bh[c] == b;
                 x = Pair{A.a0[c], A.a1[c]};
@@ -293,30 +335,109 @@ __device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs
             }
         }
         if (!valid) x = Pair{0, 0};
-        x = wave_incl_scan(x, lane);
-        uint64_t ma = sat_add(m, (m & 1) ? x.a1 : x.a0);
+        uint64_t ma = scan_from<MB>(m, x, lane);
         bool ev = act && (!valid || ma >= top || ma >= thr);
         int f = first_lane(ballot(ev));
         if (f > count) f = count;
-        if (f > 0) m = shfl(ma, f - 1);
+        if (f > 0) m = readlane64(ma, f - 1);
         pos = min(n, pos + (f << (6 * L)));
         if (f == count) { cap = 2; continue; }
-        if (L > 0) { cap = L - 1; continue; }
-        /* element event at pos: leave the binade with a real addition, or stop. */
-        uint64_t maf = shfl(ma, f);
-        float qf = shfl(qv, f);
-        cap = 2;
-        if (maf >= top) {
-            T c = join<MB>(b, m) + (T)qf;
-            if (has_thr && (double)c >= thr_v) return ResolveOut<MB>{pos, c};
-            split(c, b, m);
-            thr = has_thr ? ceil_div_pow2(thr_v, b - (MB - 1)) : kCap;
-            pos += 1;
-        } else {
-            return ResolveOut<MB>{pos, join<MB>(b, maf)};
-        }
+        cap = L - 1;                         /* descend into item f */
     }
     return ResolveOut<MB>{-1, join<MB>(b, m)};
+}
+
+/* ---- lean fp32 resolver ----------------------------------------------------
+ * The draw (src/sampler.c:226-232) accumulates in float, so m < 2^24 and every
+ * quantity fits 32 bits.  Aggregates are plain u32 increments (saturated at
+ * 2^30); a chunk or group containing a halfway case is stored as invalid, so the
+ * pair algebra is only ever needed at element level. */
+struct AggsF {
+    uint32_t *a;    /* [nch] chunk increments */
+    int *bh;        /* [nch] predicted binade or kInvalidBinade */
+    uint32_t *ga;   /* [ngr] group increments */
+    int *gbh;       /* [ngr] */
+};
+
+constexpr uint32_t kCapF = 1u << 30;
+
+/* Increment of q >= 0 on the grid of binade b (ulp 2^(b-23)); tie = halfway. */
+DLK_DEV uint32_t increment_f(float q, int b, bool &tie) {
+    float xs = ldexpf(q, 23 - b);                 /* exact power-of-two scaling */
+    tie = xs < 0x1p24f && (xs - floorf(xs)) == 0.5f;
+    return xs >= 0x1p25f ? (1u << 25) : (uint32_t)rintf(xs);
+}
+
+DLK_DEV uint32_t thr_f(double v, int b) {
+    uint64_t t = ceil_div_pow2(v, b - 23);
+    return t > kCapF ? kCapF : (uint32_t)t;
+}
+
+/* Sequential float running sum of 64 lane values in lane order, exactly as a
+ * scalar loop computes it: lane j ends with fl(...fl(fl(c + q_0) + q_1)... + q_j).
+ * Each step shifts the partial sums one lane up (DPP wave_shr:1, lane 0 reads 0)
+ * and adds the lane's own value; after `steps` steps lanes 0..steps-1 are final. */
+constexpr int kDppWaveShr1 = 0x138;
+DLK_DEV float wave_serial_sum(float c, float q, int steps) {
+    const int lane = lane_id();
+    const float q0 = lane == 0 ? c + q : q;
+    float y = q0;
+    for (int t = 1; t < steps; t++)
+        y = u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(y), kDppWaveShr1, 0xf, 0xf, true)) + q0;
+    return y;
+}
+
+/* First position (from 0) where the running float sum c0 + q(0) + ... + q(pos),
+ * accumulated left to right, reaches thr_v; aggregate levels skip whole chunks
+ * or groups whose increments are exact integers in one binade, and any other
+ * chunk is summed element by element with wave_serial_sum. */
+template <class QF>
+__device__ __forceinline__ ResolveOut<24> resolve_f(int n, const QF &q, const AggsF &A, double thr_v, float c0) {
+    const int lane = lane_id();
+    const uint32_t top = 1u << 24;
+    const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
+    int b;
+    uint64_t m64;
+    split(c0, b, m64);
+    uint32_t m = (uint32_t)m64;
+    uint32_t thr = thr_f(thr_v, b);
+    int pos = 0, cap = 2;
+    while (pos < n) {
+        int L = 0;
+        if (cap >= 2 && (pos & 4095) == 0) L = 2;
+        else if (cap >= 1 && (pos & 63) == 0) L = 1;
+        if (L == 0) {
+            const int count = min(64 - (pos & 63), n - pos);
+            const float qv = lane < count ? q(pos + lane) : 0.0f;
+            const float y = wave_serial_sum(join_f(b, m), qv, count);
+            const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
+            if (f < count) return ResolveOut<24>{pos + f, readlanef(y, f)};
+            split(readlanef(y, count - 1), b, m64);
+            m = (uint32_t)m64;
+            thr = thr_f(thr_v, b);
+            pos += count;
+            cap = 2;
+            continue;
+        }
+        const int item = pos >> (6 * L);
+        const int count = L == 2 ? min(64, ngr - item) : min(64 - (item & 63), nch - item);
+        const bool act = lane < count;
+        uint32_t a = 0;
+        bool valid = true;
+        if (act) {
+            if (L == 1) { valid = A.bh[item + lane] == b; a = A.a[item + lane]; }
+            else { valid = A.gbh[item + lane] == b; a = A.ga[item + lane]; }
+        }
+        const uint32_t ma = m + wave_scan_sat_u32(valid ? a : 0u, kCapF);
+        const bool ev = act && (!valid || ma >= top || ma >= thr);
+        int f = first_lane(ballot(ev));
+        if (f > count) f = count;
+        if (f > 0) m = (uint32_t)__builtin_amdgcn_readlane((int)ma, f - 1);
+        pos = min(n, pos + (f << (6 * L)));
+        if (f == count) { cap = 2; continue; }
+        cap = L - 1;
+    }
+    return ResolveOut<24>{-1, join_f(b, m)};
 }
 
 }  // namespace dlk

@@ -8,7 +8,7 @@
 
 namespace dlk {
 
-constexpr int kFullThreads = 512;
+constexpr int kFullThreads = 1024;
 constexpr int kFullMaxG = 16;        /* workgroups per row */
 constexpr int kPubWords = 16;        /* 64-bit words each workgroup publishes */
 constexpr int kCandSlots = 2;        /* predicted top-p crossing chunks per workgroup */

@@ -124,7 +124,7 @@ struct QSlice {
 };
 
 template <int EPT>
-__global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
+__global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
     const int G = f.G, T = kFullThreads;
@@ -181,13 +181,16 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
     for (int i = t; i < S / 32; i += T) sbits[i] = 0;
     if (t == 0) misc[0] = 0;
     __syncthreads();
+    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
+    for (int i = t; i < nh; i += T) hl[i] = hist[i];
+    __syncthreads();
     for (int i = t; i < nh; i += T) {
-        int id = hist[i];
+        int id = hl[i];
         if (id < s0 || id >= s1) continue;
         bool first = true;
         int cnt = 0;
         for (int j = 0; j < nh; j++) {
-            int o = hist[j];
+            int o = hl[j];
             if (o == id) { cnt++; if (j < i) first = false; }
         }
         if (!first) continue;
@@ -212,21 +215,22 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
     __syncthreads();
     const int np = min(misc[0], p.plan.hcap);
 
-    /* ---- stream the slice into registers -------------------------------- */
+    /* ---- stream the slice into registers: every load issued before any use */
     float v[EPT];
+    float4 raw[EPT / 4];
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
+    }
     float tm = -INFINITY;
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int i0 = s0 + 4 * (t + j4 * T);
-        float4 x4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (i0 + 3 < s1) {
-            x4 = *(const float4 *)(lg + i0);
-        } else {
-            if (i0 < s1) x4.x = lg[i0];
-            if (i0 + 1 < s1) x4.y = lg[i0 + 1];
-            if (i0 + 2 < s1) x4.z = lg[i0 + 2];
+        float xs[4] = {raw[j4].x, raw[j4].y, raw[j4].z, raw[j4].w};
+        if (!(i0 + 3 < s1)) {
+            for (int c = 0; c < 4; c++) xs[c] = i0 + c < s1 ? lg[i0 + c] : -INFINITY;
         }
-        float xs[4] = {x4.x, x4.y, x4.z, x4.w};
         uint32_t mw = 0xffffffffu;
         if (mk && i0 < s1) mw = mk[i0 >> 5] >> (i0 & 31);
         uint32_t pb = 0;
@@ -280,8 +284,8 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
-        for (int m = 1; m < 16; m <<= 1) d += shfl_xor(d, m);
-        if ((lane & 15) == 0) ce[(t + j4 * T) >> 4] = d;
+        d = row_scan_d(d);
+        if ((lane & 15) == 15) ce[(t + j4 * T) >> 4] = d;
     }
     __syncthreads();
     block_excl_scan(ce, nch, L.red);                        /* ce[c]: e prefix at chunk c; ce[nch]: slice sum */
@@ -326,8 +330,8 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
 #pragma unroll
         for (int j4 = 0; j4 < EPT / 4; j4++) {
             double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
-            for (int m = 1; m < 16; m <<= 1) d += shfl_xor(d, m);
-            if ((lane & 15) == 0) cp[(t + j4 * T) >> 4] = d;
+            d = row_scan_d(d);
+            if ((lane & 15) == 15) cp[(t + j4 * T) >> 4] = d;
         }
         __syncthreads();
         block_excl_scan(cp, nch, L.red);
@@ -499,11 +503,9 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
                 sum += n;
             }
         }
-        for (int m = 1; m < 16; m <<= 1) {
-            sum += shfl_xor(sum, m);
-            tie |= shfl_xor((int)tie, m) != 0;
-        }
-        if ((lane & 15) == 0) {
+        sum = row_scan_u32(sum);
+        tie = ((ballot(tie) >> (lane & 48)) & 0xffffull) != 0;
+        if ((lane & 15) == 15) {
             A.a0[c] = sum;
             A.a1[c] = sum;
             A.bh[c] = (valid && !tie) ? bh : kInvalidBinade;
@@ -539,7 +541,7 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
                     (a * (1.0 - mu) <= vthr && vthr <= b * (1.0 + mu)) ||
                     (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
         int sl = -1;
-        if (want && s0 + 64 * c < s1) {
+        if (want && s0 + 64 * c < s1 && s0 + 64 * c <= x) {
             sl = atomicAdd(&misc[10], 1);
             if (sl >= f.stage_cap) sl = -1;
         }
@@ -609,10 +611,10 @@ __global__ __launch_bounds__(kFullThreads, 1) void full_kernel(FullParams f) {
 
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
     using namespace dlk;
-    const void *fns[5] = {(const void *)full_kernel<32>, (const void *)full_kernel<48>, (const void *)full_kernel<64>,
-                          (const void *)full_kernel<80>, (const void *)full_kernel<96>};
+    const void *fns[5] = {(const void *)full_kernel<16>, (const void *)full_kernel<24>, (const void *)full_kernel<32>,
+                          (const void *)full_kernel<40>, (const void *)full_kernel<48>};
     static int set[5] = {0, 0, 0, 0, 0};
-    int which = ept == 32 ? 0 : ept == 48 ? 1 : ept == 64 ? 2 : ept == 80 ? 3 : ept == 96 ? 4 : -1;
+    int which = ept == 16 ? 0 : ept == 24 ? 1 : ept == 32 ? 2 : ept == 40 ? 3 : ept == 48 ? 4 : -1;
     if (which < 0) return -1;
     if (!set[which]) {
         if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
@@ -628,9 +630,9 @@ extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ep
 
 extern "C" int dlk_full_kernel_capacity(int ept, size_t lds) {
     using namespace dlk;
-    const void *fn = ept == 32 ? (const void *)full_kernel<32> : ept == 48 ? (const void *)full_kernel<48>
-                   : ept == 64 ? (const void *)full_kernel<64> : ept == 80 ? (const void *)full_kernel<80>
-                               : (const void *)full_kernel<96>;
+    const void *fn = ept == 16 ? (const void *)full_kernel<16> : ept == 24 ? (const void *)full_kernel<24>
+                   : ept == 32 ? (const void *)full_kernel<32> : ept == 40 ? (const void *)full_kernel<40>
+                               : (const void *)full_kernel<48>;
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return 0;
     int per_cu = 0, dev = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kFullThreads, lds) != hipSuccess) return 0;

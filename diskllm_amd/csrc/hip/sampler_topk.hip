@@ -92,13 +92,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     for (int i = t; i < f.S / 32; i += T) sbits[i] = 0;
     if (t == 0) misc[0] = 0;
     __syncthreads();
-    for (int i = t; i < nh; i += T) {          /* in-slice occurrences, first occurrence only */
-        int id = hist[i];
+    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
+    for (int i = t; i < nh; i += T) hl[i] = hist[i];
+    __syncthreads();
+    for (int i = t; i < nh; i += T) {             /* in-slice occurrences, first occurrence only */
+        int id = hl[i];
         if (id < s0 || id >= s1) continue;
         bool first = true;
         int cnt = 0;
         for (int j = 0; j < nh; j++) {
-            int o = hist[j];
+            int o = hl[j];
             if (o == id) { cnt++; if (j < i) first = false; }
         }
         if (!first) continue;
