@@ -143,6 +143,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     using namespace dlk;
     const int T = kFullThreads;
     if (p.greedy || p.topk_on || p.minp_on) return 1;
+    if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     if (vocab < 8192) return 1;
     int G = (256 + rows - 1) / rows;
@@ -154,17 +155,19 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     if (G > kFullMaxG) return 1;
     const int S = ept * T;
     if (p.n_out > S) return 1;
-    const int nch = S / 64, ngr = (nch + 63) / 64;
+    const int nch = S / 64;
     FullParams f;
     memset(&f, 0, sizeof(f));
     f.G = G;
     f.S = S;
     f.stage_cap = 160;
     f.force_exact = force_exact;
-    size_t lds = fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
-                 2 * r16((size_t)nch * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)ngr * 8) + r16((size_t)ngr * 4) +
-                 r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) +
-                 r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
+    /* carve order of full_kernel: sbits, spre, ce, cp, cbh, ca, rtot, rnext, rend, rpre, Pc, smap, svals, pc,
+     * misc, md */
+    size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
+                 4 * r16((size_t)nch * 4) + 2 * r16((size_t)nch * 8) + r16((size_t)(nch + 1) * 8) +
+                 r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) + r16((size_t)G * kPubWords * 8) +
+                 r16(64 * 4) + r16(16 * 8);
     if (lds > kMaxLds) return 1;
     int cap = dlk_full_kernel_capacity(ept, lds);
     int rows_per = cap / G;

@@ -347,95 +347,82 @@ __device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs
     return ResolveOut<MB>{-1, join<MB>(b, m)};
 }
 
-/* ---- lean fp32 resolver ----------------------------------------------------
- * The draw (src/sampler.c:226-232) accumulates in float, so m < 2^24 and every
- * quantity fits 32 bits.  Aggregates are plain u32 increments (saturated at
- * 2^30); a chunk or group containing a halfway case is stored as invalid, so the
- * pair algebra is only ever needed at element level. */
-struct AggsF {
-    uint32_t *a;    /* [nch] chunk increments */
-    int *bh;        /* [nch] predicted binade or kInvalidBinade */
-    uint32_t *ga;   /* [ngr] group increments */
-    int *gbh;       /* [ngr] */
+/* ---- run-skipping float resolver ------------------------------------------
+ * The draw (src/sampler.c:226-232) accumulates in float.  Chunks (64 elements)
+ * whose running value provably stays in one binade b add exact integers on the
+ * grid 2^(b-23); consecutive such chunks of one binade form a run, and for each
+ * chunk the integer total from it to the end of its run is precomputed, so the
+ * walk crosses a run in one step.  Every other chunk (binade change, halfway
+ * case, misprediction) is summed element by element in float. */
+struct Runs {
+    const int *bh;          /* [nch] binade of the chunk, or kInvalidBinade */
+    const uint64_t *tot;    /* [nch] increments from the chunk to the end of its run */
+    const int *next;        /* [nch] first chunk after the run */
 };
 
-constexpr uint32_t kCapF = 1u << 30;
-
-/* Increment of q >= 0 on the grid of binade b (ulp 2^(b-23)); tie = halfway. */
-DLK_DEV uint32_t increment_f(float q, int b, bool &tie) {
-    float xs = ldexpf(q, 23 - b);                 /* exact power-of-two scaling */
-    tie = xs < 0x1p24f && (xs - floorf(xs)) == 0.5f;
-    return xs >= 0x1p25f ? (1u << 25) : (uint32_t)rintf(xs);
-}
-
-DLK_DEV uint32_t thr_f(double v, int b) {
-    uint64_t t = ceil_div_pow2(v, b - 23);
-    return t > kCapF ? kCapF : (uint32_t)t;
-}
-
-/* Sequential float running sum of 64 lane values in lane order, exactly as a
- * scalar loop computes it: lane j ends with fl(...fl(fl(c + q_0) + q_1)... + q_j).
- * Each step shifts the partial sums one lane up (DPP wave_shr:1, lane 0 reads 0)
- * and adds the lane's own value; after `steps` steps lanes 0..steps-1 are final. */
 constexpr int kDppWaveShr1 = 0x138;
-DLK_DEV float wave_serial_sum(float c, float q, int steps) {
-    const int lane = lane_id();
-    const float q0 = lane == 0 ? c + q : q;
+
+/* Running float sum of the 64 lane values in lane order, exactly as a scalar
+ * loop computes it: lane j ends with fl(...fl(fl(c + q_0) + q_1)... + q_j).
+ * Each step shifts the partial sums one lane up (DPP wave_shr:1, lane 0 reads
+ * 0) and adds the lane's own value; after step t lanes 0..t are final. */
+DLK_DEV float wave_serial_sum(float c, float q) {
+    const float q0 = lane_id() == 0 ? c + q : q;
     float y = q0;
-    for (int t = 1; t < steps; t++)
+#pragma unroll
+    for (int t = 1; t < 64; t++)
         y = u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(y), kDppWaveShr1, 0xf, 0xf, true)) + q0;
     return y;
 }
 
-/* First position (from 0) where the running float sum c0 + q(0) + ... + q(pos),
- * accumulated left to right, reaches thr_v; aggregate levels skip whole chunks
- * or groups whose increments are exact integers in one binade, and any other
- * chunk is summed element by element with wave_serial_sum. */
+/* First position pos < n where the running float sum c0 + q(0) + ... + q(pos)
+ * reaches thr_v, and the running value there; {-1, final value} if none.
+ * Elements past n in the last chunk and in run totals must be zero. */
 template <class QF>
-__device__ __forceinline__ ResolveOut<24> resolve_f(int n, const QF &q, const AggsF &A, double thr_v, float c0) {
+__device__ __forceinline__ ResolveOut<24> resolve_runs(int n, const QF &q, const Runs &R, double thr_v, float c0) {
     const int lane = lane_id();
-    const uint32_t top = 1u << 24;
-    const int nch = (n + 63) >> 6, ngr = (nch + 63) >> 6;
+    const int nch = (n + 63) >> 6;
     int b;
-    uint64_t m64;
-    split(c0, b, m64);
-    uint32_t m = (uint32_t)m64;
-    uint32_t thr = thr_f(thr_v, b);
-    int pos = 0, cap = 2;
-    while (pos < n) {
-        int L = 0;
-        if (cap >= 2 && (pos & 4095) == 0) L = 2;
-        else if (cap >= 1 && (pos & 63) == 0) L = 1;
-        if (L == 0) {
-            const int count = min(64 - (pos & 63), n - pos);
-            const float qv = lane < count ? q(pos + lane) : 0.0f;
-            const float y = wave_serial_sum(join_f(b, m), qv, count);
-            const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
-            if (f < count) return ResolveOut<24>{pos + f, readlanef(y, f)};
-            split(readlanef(y, count - 1), b, m64);
-            m = (uint32_t)m64;
-            thr = thr_f(thr_v, b);
-            pos += count;
-            cap = 2;
-            continue;
+    uint64_t m;
+    split(c0, b, m);
+    uint64_t thr = ceil_div_pow2(thr_v, b - 23);
+    int j = 0;
+    while (j < nch) {
+        if (R.bh[j] == b) {
+            const uint64_t lim = thr < (1ull << 24) ? thr : (1ull << 24);
+            uint64_t tot = R.tot[j];
+            const int nx = R.next[j];
+            if (m + tot < lim) {
+                m += tot;
+                j = nx;
+                continue;
+            }
+            /* the limit is reached inside the run: find the chunk */
+            while (true) {
+                const int k = j + lane;
+                const uint64_t tk = k < nx ? R.tot[k] : 0;
+                const uint64_t tk1 = k + 1 < nx ? R.tot[k + 1] : 0;
+                const int f = first_lane(ballot(k < nx && m + (tot - tk1) >= lim));
+                if (f < 64) {
+                    m += tot - readlane64(tk, f);
+                    j += f;
+                    break;
+                }
+                const uint64_t tn = readlane64(tk1, 63);
+                m += tot - tn;
+                tot = tn;
+                j += 64;
+            }
         }
-        const int item = pos >> (6 * L);
-        const int count = L == 2 ? min(64, ngr - item) : min(64 - (item & 63), nch - item);
-        const bool act = lane < count;
-        uint32_t a = 0;
-        bool valid = true;
-        if (act) {
-            if (L == 1) { valid = A.bh[item + lane] == b; a = A.a[item + lane]; }
-            else { valid = A.gbh[item + lane] == b; a = A.ga[item + lane]; }
-        }
-        const uint32_t ma = m + wave_scan_sat_u32(valid ? a : 0u, kCapF);
-        const bool ev = act && (!valid || ma >= top || ma >= thr);
-        int f = first_lane(ballot(ev));
-        if (f > count) f = count;
-        if (f > 0) m = (uint32_t)__builtin_amdgcn_readlane((int)ma, f - 1);
-        pos = min(n, pos + (f << (6 * L)));
-        if (f == count) { cap = 2; continue; }
-        cap = L - 1;
+        const int base = j * 64;
+        const int count = min(64, n - base);
+        const float qv = lane < count ? q(base + lane) : 0.0f;
+        const float y = wave_serial_sum(join_f(b, m), qv);
+        const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
+        if (f < count) return ResolveOut<24>{base + f, readlanef(y, f)};
+        split(readlanef(y, count - 1), b, m);
+        thr = ceil_div_pow2(thr_v, b - 23);
+        j++;
     }
     return ResolveOut<24>{-1, join_f(b, m)};
 }

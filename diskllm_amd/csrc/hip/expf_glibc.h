@@ -48,34 +48,41 @@ DLK_HD uint64_t dlk_d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
 DLK_HD float dlk_u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 DLK_HD uint32_t dlk_f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 
-/* exp(x) for float x, bit-identical to glibc 2.35 expf (x86-64 FMA variant). */
-DLK_HD float dlk_expf_glibc(float x, const uint64_t *tab) {
+/* The general formula of glibc 2.35 expf (x86-64 FMA variant) without its
+ * special-case screen: exact for finite x in [-1000, 88.72] (below -103.97 it
+ * rounds to 0 like the screened path), branch-free so loops interleave. */
+DLK_HD float dlk_expf_glibc_core(float x, const uint64_t *tab) {
     const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
     const double kShift = 0x1.8p+52;
     const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
     const double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
-    uint32_t ux = dlk_f2u(x);
-    uint32_t abstop = (ux >> 20) & 0x7ff;
+    const double xd = (double)x;
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = dlk_d2u(kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const uint64_t t = tab[ki & 31] + (ki << 47);
+    const double s = dlk_u2d(t);
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+/* exp(x) for float x, bit-identical to glibc 2.35 expf (x86-64 FMA variant). */
+DLK_HD float dlk_expf_glibc(float x, const uint64_t *tab) {
+    const uint32_t ux = dlk_f2u(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
     if (abstop >= 0x42bu) {                         /* |x| >= 88 or NaN */
         if (ux == 0xff800000u) return 0.0f;         /* -inf */
         if (abstop >= 0x7f8u) return x + x;         /* +inf, NaN */
         if (x > 0x1.62e42ep6f) return dlk_u2f(0x7f800000u);
         if (x < -0x1.9fe368p6f) return 0.0f;
     }
-    double xd = (double)x;
-    double kd = __builtin_fma(kInvLn2N, xd, kShift);
-    uint64_t ki = dlk_d2u(kd);
-    kd -= kShift;
-    double r = __builtin_fma(kInvLn2N, xd, -kd);
-    uint64_t t = tab[ki & 31] + (ki << 47);
-    double s = dlk_u2d(t);
-    double z = __builtin_fma(kC0, r, kC1);
-    double r2 = r * r;
-    double y = __builtin_fma(kC2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
+    return dlk_expf_glibc_core(x, tab);
 }
 
 #endif

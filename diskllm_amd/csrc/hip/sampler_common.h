@@ -177,6 +177,26 @@ __device__ __forceinline__ int block_sum_int(int v, Lds &L) {
  * the mask first (grammar runs before the penalties, src/core/sampler_api.c:51-61),
  * then the ops in `order`; repetition is applied once per occurrence
  * (src/sampler.c:23-31), presence and frequency once per distinct id. */
+/* Penalties of one logit whose id occurs `cnt` times in the history, in the
+ * configured order (src/sampler.c:19-63 and the builder's frequency/presence
+ * pass): repetition divides positive / multiplies negative logits once per
+ * occurrence; frequency subtracts freq * count; presence subtracts pres once. */
+DLK_DEV float penalize(float x, int cnt, const RowParams &p) {
+    for (int s = 0; s < 8; s++) {
+        uint32_t op = (p.order >> (4 * s)) & 0xFu;
+        if (op == 0) break;
+        if (op == DLK_OP_REPETITION) {
+            if (p.rep > 1.0f)
+                for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
+        } else if (op == DLK_OP_FREQUENCY) {
+            if (p.freq != 0.0f) { float d = p.freq * (float)cnt; x = x - d; }
+        } else if (op == DLK_OP_PRESENCE) {
+            if (p.pres != 0.0f) x = x - p.pres;
+        }
+    }
+    return x;
+}
+
 __device__ __forceinline__ int build_patches(const RowParams &p, int row, const float *lg, const uint32_t *mk, Lds &L,
                              const LdsPlan &pl, int V) {
     const int t = threadIdx.x, T = blockDim.x;
@@ -229,21 +249,7 @@ __device__ __forceinline__ int build_patches(const RowParams &p, int row, const 
         int cnt = (int)L.pval[j];
         float x = lg[id];
         if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-        for (int s = 0; s < 8; s++) {
-            uint32_t op = (p.order >> (4 * s)) & 0xFu;
-            if (op == 0) break;
-            if (op == DLK_OP_REPETITION) {
-                if (p.rep > 1.0f)
-                    for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
-            } else if (op == DLK_OP_FREQUENCY) {
-                if (p.freq != 0.0f) {
-                    float d = p.freq * (float)cnt;
-                    x = x - d;
-                }
-            } else if (op == DLK_OP_PRESENCE) {
-                if (p.pres != 0.0f) x = x - p.pres;
-            }
-        }
+        x = penalize(x, cnt, p);
         L.pval[j] = x;
         atomicOr(&L.pflag[id >> 11], 1u << ((id >> 6) & 31));
     }

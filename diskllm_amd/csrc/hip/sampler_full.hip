@@ -2,8 +2,8 @@
  * sampler_full.hip -- fused full-vocabulary sampling (top-k off, min-p off):
  * src/sampler.c:136-234 with k = V, bit-exact, one HBM pass.
  *
- * A row is split over G workgroups (cooperative launch, so all of a row's
- * workgroups are resident); each keeps its slice in registers.  The row is
+ * A row is split over G workgroups, all resident at once (see
+ * dlk_launch_full_kernel); each keeps its slice in registers.  The row is
  * tied together by three row barriers and a chain, all through relaxed
  * agent-scope atomics (every shared word is an atomic store/load; each writer
  * waits for its stores before it signals, so no cache-flushing fences are needed):
@@ -31,7 +31,7 @@
 
 namespace dlk {
 
-constexpr uint32_t kSpinLimit = 1u << 24;
+constexpr uint32_t kSpinLimit = 1u << 22;   /* bounded waits: a few seconds at most */
 
 DLK_DEV void at_st32(uint32_t *a, uint32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DLK_DEV void at_st64(uint64_t *a, uint64_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -94,6 +94,40 @@ __device__ __forceinline__ void block_excl_scan(double *P, int n, double *red) {
     __syncthreads();
 }
 
+/* Rank of marked bit li among the marked bits before it. */
+DLK_DEV int slice_rank(const uint32_t *bits, const uint32_t *pre, int li) {
+    return (int)pre[li >> 5] + __popc(bits[li >> 5] & ((1u << (li & 31)) - 1u));
+}
+
+/* Exclusive prefix of per-thread counts in thread order (red: 16 words). */
+DLK_DEV uint32_t block_excl_prefix_u32(uint32_t v, uint32_t *red) {
+    const int lane = lane_id(), w = wave_id();
+    const uint32_t inc = wave_scan_sat_u32(v, 0xffffffffu);
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int k = 0; k < w; k++) base += red[k];
+    __syncthreads();
+    return base + inc - v;
+}
+
+/* Inclusive prefix of per-thread 64-bit values in thread order (red: 16 words). */
+DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
+    const int lane = lane_id(), w = wave_id();
+    uint64_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t o = shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    uint64_t base = 0;
+    for (int k = 0; k < w; k++) base += red[k];
+    __syncthreads();
+    return base + inc;
+}
+
 /* Element values of the draw inside one slice: staged chunks from LDS, anything
  * else recomputed from the logits exactly as the registers held it. */
 struct QSlice {
@@ -102,9 +136,9 @@ struct QSlice {
     const float *lg;
     const uint32_t *mk;
     const uint32_t *sbits;
-    const int *pid;
+    const uint32_t *spre;
     const float *pval;
-    int np, s0, x, topp;
+    int s0, x, topp;
     float M, inv_t, inv, inv3;
     const uint64_t *tab;
     DLK_DEV float operator()(int i) const {
@@ -114,9 +148,7 @@ struct QSlice {
         if (gi > x) return 0.0f;
         float l = lg[gi];
         if (mk && !((mk[gi >> 5] >> (gi & 31)) & 1u)) l = -INFINITY;
-        if ((sbits[i >> 5] >> (i & 31)) & 1u)
-            for (int k = 0; k < np; k++)
-                if (pid[k] == gi) l = pval[k];
+        if ((sbits[i >> 5] >> (i & 31)) & 1u) l = pval[slice_rank(sbits, spre, i)];
         float e = dlk_expf_glibc((l - M) * inv_t, tab);
         float pj = e * inv;
         return topp ? pj * inv3 : pj;
@@ -130,7 +162,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const int G = f.G, T = kFullThreads;
     const int row = blockIdx.x / G, g = blockIdx.x % G;
     const int t = threadIdx.x, lane = lane_id();
-    const int V = p.V, S = f.S, nch = S / 64, ngr = (nch + 63) / 64;
+    const int V = p.V, S = f.S, nch = S / 64;
     const int s0 = g * S, s1 = min(V, s0 + S);
     const float *lg = p.logits + (int64_t)row * p.ld;
     const uint32_t *mk = nullptr;
@@ -143,16 +175,16 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     Lds L = make_lds(smem, p.plan);
     unsigned char *q = L.region;
     uint32_t *sbits = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
+    uint32_t *spre = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
     double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);
     double *cp = (double *)carve(q, (size_t)(nch + 1) * 8);
-    Aggs A;
-    A.a0 = (uint64_t *)carve(q, (size_t)nch * 8);
-    A.a1 = (uint64_t *)carve(q, (size_t)nch * 8);
-    A.bh = (int *)carve(q, (size_t)nch * 4);
-    A.ga0 = (uint64_t *)carve(q, (size_t)ngr * 8);
-    A.ga1 = (uint64_t *)carve(q, (size_t)ngr * 8);
-    A.gbh = (int *)carve(q, (size_t)ngr * 4);
-    A.P = (double *)carve(q, (size_t)(nch + 1) * 8);
+    int *cbh = (int *)carve(q, (size_t)nch * 4);                 /* chunk binade or kInvalidBinade */
+    uint32_t *ca = (uint32_t *)carve(q, (size_t)nch * 4);        /* chunk increments on that grid */
+    uint64_t *rtot = (uint64_t *)carve(q, (size_t)nch * 8);      /* increments to the end of the run */
+    int *rnext = (int *)carve(q, (size_t)nch * 4);               /* first chunk after the run */
+    int *rend = (int *)carve(q, (size_t)nch * 4);                /* scratch: last chunk of run r */
+    uint64_t *rpre = (uint64_t *)carve(q, (size_t)nch * 8);      /* scratch: increments up to it */
+    double *Pc = (double *)carve(q, (size_t)(nch + 1) * 8);      /* predicted running value */
     int *smap = (int *)carve(q, (size_t)nch * 4);
     float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
     uint64_t *pc = (uint64_t *)carve(q, (size_t)G * kPubWords * 8);   /* published words, cached */
@@ -162,6 +194,16 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
 
     const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
     const float r = rand_f32_from(st);
+
+    /* ---- stream the slice into registers: every load issued before any use */
+    float4 raw[EPT / 4];
+    uint32_t mwd[EPT / 4];
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
+        mwd[j4] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
+    }
 
     /* ---- penalty patches of the ids inside this slice ------------------- */
     const int32_t *hist = nullptr;
@@ -178,52 +220,40 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         row_exit(sync, G);
         return;
     }
-    for (int i = t; i < S / 32; i += T) sbits[i] = 0;
-    if (t == 0) misc[0] = 0;
+    const int nw = S / 32;
+    for (int i = t; i < nw; i += T) sbits[i] = 0;
+    for (int i = t; i < p.plan.hcap; i += T) L.pcnt[i] = 0;
+    if (t == 0) misc[5] = 0;
     __syncthreads();
     int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
-    for (int i = t; i < nh; i += T) hl[i] = hist[i];
-    __syncthreads();
     for (int i = t; i < nh; i += T) {
-        int id = hl[i];
-        if (id < s0 || id >= s1) continue;
-        bool first = true;
-        int cnt = 0;
-        for (int j = 0; j < nh; j++) {
-            int o = hl[j];
-            if (o == id) { cnt++; if (j < i) first = false; }
-        }
-        if (!first) continue;
-        float x = lg[id];
-        if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-        for (int s = 0; s < 8; s++) {
-            uint32_t op = (p.order >> (4 * s)) & 0xFu;
-            if (op == 0) break;
-            if (op == DLK_OP_REPETITION) {
-                if (p.rep > 1.0f)
-                    for (int k = 0; k < cnt; k++) x = x < 0.0f ? x * p.rep : x / p.rep;
-            } else if (op == DLK_OP_FREQUENCY) {
-                if (p.freq != 0.0f) { float d = p.freq * (float)cnt; x = x - d; }
-            } else if (op == DLK_OP_PRESENCE) {
-                if (p.pres != 0.0f) x = x - p.pres;
-            }
-        }
-        int at = atomicAdd(&misc[0], 1);
-        if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = x; }
-        atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
+        const int id = hist[i];
+        hl[i] = id;
+        if (id >= s0 && id < s1) atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
     }
     __syncthreads();
-    const int np = min(misc[0], p.plan.hcap);
-
-    /* ---- stream the slice into registers: every load issued before any use */
-    float v[EPT];
-    float4 raw[EPT / 4];
-#pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        const int i0 = s0 + 4 * (t + j4 * T);
-        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
+    /* patch slot of a marked id = its rank among the marked ids of the slice */
+    {
+        const int per = (nw + T - 1) / T, w0 = t * per;
+        uint32_t cnt = 0;
+        for (int k = 0; k < per; k++)
+            if (w0 + k < nw) cnt += __popc(sbits[w0 + k]);
+        uint32_t base = block_excl_prefix_u32(cnt, (uint32_t *)L.bi);
+        for (int k = 0; k < per; k++)
+            if (w0 + k < nw) { spre[w0 + k] = base; base += __popc(sbits[w0 + k]); }
+        if (t == T - 1) misc[0] = (int)base;
     }
+    __syncthreads();
+    const int np = misc[0];
+    for (int i = t; i < nh; i += T) {
+        const int id = hl[i];
+        if (id >= s0 && id < s1) atomicAdd(&L.pcnt[slice_rank(sbits, spre, id - s0)], 1);
+    }
+    __syncthreads();
+
+    float v[EPT];
     float tm = -INFINITY;
+    bool bad = false;                              /* NaN or +inf after penalties */
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int i0 = s0 + 4 * (t + j4 * T);
@@ -231,39 +261,48 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         if (!(i0 + 3 < s1)) {
             for (int c = 0; c < 4; c++) xs[c] = i0 + c < s1 ? lg[i0 + c] : -INFINITY;
         }
-        uint32_t mw = 0xffffffffu;
-        if (mk && i0 < s1) mw = mk[i0 >> 5] >> (i0 & 31);
+        const uint32_t mw = mwd[j4] >> (i0 & 31);
+        const int li0 = i0 - s0;
         uint32_t pb = 0;
-        if (i0 < s1) pb = (sbits[(i0 - s0) >> 5] >> ((i0 - s0) & 31)) & 0xFu;
+        if (i0 < s1) pb = (sbits[li0 >> 5] >> (li0 & 31)) & 0xFu;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int i = i0 + c;
             float x = xs[c];
             if (!((mw >> c) & 1u)) x = -INFINITY;
-            if ((pb >> c) & 1u)
-                for (int k = 0; k < np; k++)
-                    if (L.pid[k] == i) x = L.pval[k];
+            if ((pb >> c) & 1u) {
+                const int slot = slice_rank(sbits, spre, li0 + c);
+                x = penalize(x, L.pcnt[slot], p);
+                L.pval[slot] = x;
+            }
             if (i >= s1) x = -INFINITY;
             v[j4 * 4 + c] = x;
             tm = fmaxf(tm, x);
+            bad |= !(x < INFINITY) && !(x == -INFINITY);
         }
     }
+    if (ballot(bad) != 0 && lane == 0) misc[5] = 1;
 
     /* ---- A: row maximum -------------------------------------------------- */
     {
         int dummy = 0;
         block_argmax(tm, dummy, L);
     }
-    if (t == 0) at_st64(&mypub[kPubMax], f2u(tm));
+    if (t == 0) at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
     row_barrier(&sync[kSyncA], G, p.status);
     if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubMax]);
     __syncthreads();
     float M = -INFINITY;
-    for (int h = 0; h < G; h++) M = fmaxf(M, u2f((uint32_t)pc[h]));
+    bool row_bad = false;
+    for (int h = 0; h < G; h++) {
+        M = fmaxf(M, u2f((uint32_t)pc[h]));
+        row_bad |= (pc[h] >> 32) != 0;
+    }
     if (g == 0 && t == 0) p.rng[row] = st;                  /* every workgroup has read it */
     const int n_out = p.n_out;
-    if (!(M > -INFINITY)) {
-        /* every entry -inf: NaN softmax, the draw falls through to index V-1 */
+    if (row_bad || !(M > -INFINITY)) {
+        /* every entry -inf, or a NaN / +inf entry: the softmax sum is NaN, no
+         * comparison with it holds, and the draw falls through to index V-1 */
         if (g == 0) {
             if (t == 0) p.out_ids[row] = V - 1;
             for (int j = t; j < n_out; j += T) {
@@ -280,12 +319,19 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     /* ---- e and its slice sums ------------------------------------------- */
     const float inv_t = p.inv_temp;
 #pragma unroll
-    for (int j = 0; j < EPT; j++) v[j] = dlk_expf_glibc((v[j] - M) * inv_t, L.tab);
-#pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
-        double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
+        /* four at a time, each group summed at once: enough independent work
+         * to hide latency without widening live ranges into spills */
+        double d = 0.0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float e = dlk_expf_glibc_core(fmaxf((v[4 * j4 + k] - M) * inv_t, -200.0f), L.tab);
+            v[4 * j4 + k] = e;
+            d = k == 0 ? (double)e : d + (double)e;
+        }
         d = row_scan_d(d);
         if ((lane & 15) == 15) ce[(t + j4 * T) >> 4] = d;
+        __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
     block_excl_scan(ce, nch, L.red);                        /* ce[c]: e prefix at chunk c; ce[nch]: slice sum */
@@ -383,7 +429,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         row_barrier(&sync[kSyncC], G, p.status);
         if (t < G * kPubWords) pc[t] = at_ld64(&pubrow[t]);
         __syncthreads();
-        if (t == 0) {
+        if (wave_id() == 0) {
+            /* one wave: each candidate chunk's running sum by a wave scan; any
+             * summation order is fine, the bound e covers the difference */
             int okc = 1, xx = V - 1;
             float i3 = 1.0f;
             if (!topp) {
@@ -395,22 +443,27 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 double RW = 0.0, s3 = 0.0, eps3 = 0.0;
                 bool found = false;
                 for (int h = 0; h < G && okc && !found; h++) {
-                    uint64_t nc = pc[h * kPubWords + kPubNCand];
+                    const uint64_t nc = pc[h * kPubWords + kPubNCand];
                     if (nc == 0xffffull) { okc = 0; break; }
                     for (int s = 0; s < (int)nc && okc && !found; s++) {
-                        int cg = (int)pc[h * kPubWords + kPubCandChunk + s];
-                        double R = RW + u2d(pc[h * kPubWords + kPubCandPre + s]);
+                        const int cg = (int)pc[h * kPubWords + kPubCandChunk + s];
+                        const double R0 = RW + u2d(pc[h * kPubWords + kPubCandPre + s]);
                         const float *vals = f.cvals + ((int64_t)row * G + h) * kCandSlots * 64 + s * 64;
-                        for (int k = 0; k < 64; k++) {
-                            int i = cg * 64 + k;
-                            if (i >= V) break;
-                            R += (double)u2f(at_ld32((const uint32_t *)&vals[k]));
-                            double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
-                            if (R * (1.0 + e) >= tau) {
-                                if (R * (1.0 - e) >= tau) { found = true; xx = i; s3 = R; eps3 = e; }
-                                else okc = 0;
-                                break;
-                            }
+                        const int i = cg * 64 + lane;
+                        double R = i < V ? (double)u2f(at_ld32((const uint32_t *)&vals[lane])) : 0.0;
+#pragma unroll
+                        for (int d = 1; d < 64; d <<= 1) {
+                            const double o = shfl_up(R, d);
+                            if (lane >= d) R += o;
+                        }
+                        R += R0;
+                        const double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
+                        const int fl = first_lane(ballot(i < V && R * (1.0 + e) >= tau));
+                        if (fl < 64) {
+                            const double Rf = u2d(readlane64(d2u(R), fl));
+                            const double ef = ((double)(cg * 64 + fl + 1) + 256.0) * U * 1.01 + 4.0 * U;
+                            if (Rf * (1.0 - ef) >= tau) { found = true; xx = cg * 64 + fl; s3 = Rf; eps3 = ef; }
+                            else okc = 0;
                         }
                     }
                     RW += u2d(pc[h * kPubWords + kPubP]);
@@ -427,7 +480,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                     else okc = 0;
                 }
             }
-            misc[8] = okc; misc[9] = xx; md[0] = (double)i3;
+            if (lane == 0) { misc[8] = okc; misc[9] = xx; md[0] = (double)i3; }
         }
         __syncthreads();
         ok = misc[8] != 0;
@@ -485,14 +538,14 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int cx = (x - s0) >> 6;
         Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + cp[min(nch, cx + 1)]);
     }
-    for (int c = t; c <= nch; c += T) A.P[c] = fmin(RWg + cp[c], Rx) * scale;
+    for (int c = t; c <= nch; c += T) Pc[c] = fmin(RWg + cp[c], Rx) * scale;
     __syncthreads();
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T;
         const int c = u >> 4;
-        int bh = predict_binade<24>(A.P[c]);
-        bool valid = bh == predict_binade<24>(A.P[c + 1]) && bh >= -100;
+        int bh = predict_binade<24>(Pc[c]);
+        bool valid = bh == predict_binade<24>(Pc[c + 1]) && bh >= -100;
         uint32_t sum = 0;
         bool tie = false;
         if (valid) {
@@ -506,28 +559,27 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         sum = row_scan_u32(sum);
         tie = ((ballot(tie) >> (lane & 48)) & 0xffffull) != 0;
         if ((lane & 15) == 15) {
-            A.a0[c] = sum;
-            A.a1[c] = sum;
-            A.bh[c] = (valid && !tie) ? bh : kInvalidBinade;
+            ca[c] = sum;
+            cbh[c] = (valid && !tie) ? bh : kInvalidBinade;
         }
     }
     if (t == 0) misc[10] = 0;
     __syncthreads();
+    /* runs: maximal stretches of valid chunks of one binade (nch <= T) */
     {
-        const int wv = wave_id();
-        for (int gr = wv; gr < ngr; gr += n_waves()) {
-            int c = gr * 64 + lane;
-            bool in = c < nch;
-            int b0 = A.bh[gr * 64];
-            bool same = !in || A.bh[c] == b0;
-            bool gok = (ballot(!same) == 0) && b0 != kInvalidBinade;
-            uint64_t sv = in ? A.a0[c] : 0;
-            for (int m = 32; m >= 1; m >>= 1) sv += shfl_xor(sv, m);
-            if (lane == 0) {
-                A.ga0[gr] = sv;
-                A.ga1[gr] = sv;
-                A.gbh[gr] = gok ? b0 : kInvalidBinade;
-            }
+        const int c = t;
+        const bool in = c < nch;
+        const int bc = in ? cbh[c] : kInvalidBinade;
+        const bool vld = bc != kInvalidBinade;
+        const bool end = in && (!vld || c == nch - 1 || cbh[c + 1] != bc);
+        const uint64_t a = vld ? (uint64_t)ca[c] : 0;
+        const uint32_t run = block_excl_prefix_u32(end ? 1u : 0u, (uint32_t *)L.bi);
+        const uint64_t ainc = block_incl_prefix_u64(a, (uint64_t *)L.red);
+        if (end) { rend[run] = c; rpre[run] = ainc; }
+        __syncthreads();
+        if (in) {
+            rnext[c] = vld ? rend[run] + 1 : c + 1;
+            rtot[c] = vld ? rpre[run] - (ainc - a) : 0;
         }
     }
     /* chunks the walk may have to open: mispredicted or near a binade edge,
@@ -535,8 +587,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const double vthr = (double)u2f(f2u(r) + 1u);
     const double mu = 0x1p-8;
     for (int c = t; c < nch; c += T) {
-        double a = A.P[c], b = A.P[c + 1];
-        bool want = A.bh[c] == kInvalidBinade ||
+        double a = Pc[c], b = Pc[c + 1];
+        bool want = cbh[c] == kInvalidBinade ||
                     predict_binade<24>(a * (1.0 - mu)) != predict_binade<24>(b * (1.0 + mu)) ||
                     (a * (1.0 - mu) <= vthr && vthr <= b * (1.0 + mu)) ||
                     (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
@@ -583,9 +635,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         c_in = u2f((uint32_t)misc[12]);
     }
     const int n_loc = min(s1, x + 1) - s0;
-    QSlice qs{smap, svals, lg, mk, sbits, L.pid, L.pval, np, s0, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
+    QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, s0, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
     if (wave_id() == 0) {
-        ResolveOut<24> o = resolve<24>(n_loc, qs, A, true, vthr, c_in);
+        ResolveOut<24> o = resolve_runs(n_loc, qs, Runs{cbh, rtot, rnext}, vthr, c_in);
         if (lane == 0) { misc[13] = o.pos; misc[14] = (int)f2u(o.value); }
     }
     __syncthreads();
@@ -621,10 +673,22 @@ extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ep
             return -1;
         set[which] = 1;
     }
-    FullParams fp = *f;
-    void *args[] = {&fp};
-    hipError_t e = hipLaunchCooperativeKernel(fns[which], dim3(rows * f->G), dim3(kFullThreads), args, (unsigned)lds,
-                                              stream);
+    /* An ordinary launch: the grid fits the device at one workgroup per CU
+     * (checked by the host against dlk_full_kernel_capacity), and the row
+     * waits only on workgroups of its own row.  Workgroups are dispatched in
+     * index order and a row's workgroups are consecutive, so every row below
+     * the dispatch frontier is fully resident and finishes, which frees room
+     * for the rest: the barriers make progress without a cooperative launch
+     * (which costs ~12 us of launch latency here), and every wait is bounded. */
+    const FullParams fp = *f;
+    switch (which) {
+        case 0: hipLaunchKernelGGL(full_kernel<16>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
+        case 1: hipLaunchKernelGGL(full_kernel<24>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
+        case 2: hipLaunchKernelGGL(full_kernel<32>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
+        case 3: hipLaunchKernelGGL(full_kernel<40>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
+        default: hipLaunchKernelGGL(full_kernel<48>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
+    }
+    const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -1;
 }
 
