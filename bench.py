@@ -29,6 +29,34 @@ BYTES_PER_ROW = VOCAB * 4 + HIST * 4 + 8 + 4      # 608,780 B
 METRIC = "sampled rows/sec + achieved HBM GB/s (% of peak), batch 64, vocab 151936"
 
 
+def fused_kernel_name(rows: int, vocab: int) -> str:
+    """Template instance of the fused full-vocabulary kernel dlk_sample launches for
+    this shape (the same selection as launch_full in diskllm_amd/csrc/hip/capi.hip:
+    G = ceil(256 / rows) workgroups per row, elements per thread rounded up to a bucket)."""
+    G = min(16, max(1, (256 + rows - 1) // rows))
+    ept = (vocab + G * 1024 - 1) // (G * 1024)
+    ept = next(e for e in (16, 24, 32, 40, 48) if ept <= e or e == 48)
+    return f"dlk::full_kernel<{ept}>"
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy of known size), or None
+    when the summary is absent or was taken on another kernel."""
+    path = os.path.join(ROOT, "profiles", "full_kernel_c2_hbm_traffic.txt")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    short = kernel.replace("dlk::", "")
+    if short not in text:
+        return None
+    for ln in text.splitlines():
+        if ln.startswith("scaled traffic per launch:"):
+            return int(round(float(ln.split("=")[-1].split()[0]) * 1e6))
+    return None
+
+
 def cpu_baseline(w, runs: int, threads_all: int) -> dict:
     """The reference src/sampler.c (strict ISO C build in oracle/_ref) on the host:
     penalties + sampler_sample for every row, rows split over pthreads."""
@@ -58,6 +86,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="instead of the benchmark, run --steps plain device-to-device copies of this many MiB "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -72,6 +103,15 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": args.steps}))
+        return 0
     w = workloads.c2()
     db = api.to_device(w, device=dev)
     params = api.params_of(w)
@@ -121,9 +161,9 @@ def main() -> int:
         "hbm_gbps": round(bytes_launch / (ms_step * 1e-3) / 1e9, 1),
         "hbm_frac": round(bytes_launch / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "parity": f"{n_ok}/{ROWS} token ids bit-identical to the oracle",
-        "roofline": {"bound": "hbm", "kernel": "dlk::row_kernel", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": fused_kernel_name(ROWS, VOCAB), "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes_per_launch": bytes_launch, "ms_per_launch": round(ms_kernel, 5)},
+                     "traffic": profiled_traffic(fused_kernel_name(ROWS, VOCAB)), "bytes_per_launch": bytes_launch, "ms_per_launch": round(ms_kernel, 5)},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
