@@ -46,10 +46,36 @@ class SamplerConfig(C.Structure):
                 ("seed", C.c_uint64)]
 
 
+GRAMMAR_NONE, GRAMMAR_JSON, GRAMMAR_RECEIPT = 0, 1, 2
+
+
+class ScanState(C.Structure):
+    _fields_ = [("mode", C.c_int32), ("pc", C.c_int32), ("n", C.c_int32), ("m", C.c_int32), ("prev", C.c_uint8),
+                ("flag", C.c_uint8), ("pad", C.c_uint8 * 2)]
+
+
+class BalanceState(C.Structure):
+    _fields_ = [("braces", C.c_int32), ("brackets", C.c_int32), ("len", C.c_int32), ("in_str", C.c_uint8),
+                ("prev", C.c_uint8), ("pad", C.c_uint8 * 2)]
+
+
+class GrammarRow(C.Structure):
+    """dlk_grammar_row (include/diskllm_amd.h)."""
+    _fields_ = [("scan", ScanState), ("bal", BalanceState)]
+
+
 # Every symbol the public headers declare (checked by the CPU test suite).
 EXPORTS = [
     # include/diskllm_amd.h
-    "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf",
+    "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
+    "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask",
+    # include/sampler.h
+    "sampler_create", "sampler_free", "sampler_apply_repetition_penalty", "sampler_apply_presence_penalty",
+    "sampler_sample", "greedy_sample",
+    # include/grammar.h
+    "diskllm_grammar_init_from_file", "diskllm_grammar_init_from_str", "diskllm_grammar_init_json",
+    "diskllm_grammar_free", "diskllm_grammar_reset", "diskllm_grammar_accept_str", "diskllm_grammar_advance",
+    "diskllm_grammar_is_finished", "diskllm_grammar_apply_mask",
 ]
 
 
@@ -81,6 +107,41 @@ def lib() -> C.CDLL:
                                    C.c_int, C.c_uint64, C.c_void_p, C.c_int64, C.c_void_p]
         L.dlk_expf.restype = C.c_int
         L.dlk_expf.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+        L.dlk_apply_penalties.restype = C.c_int
+        L.dlk_apply_penalties.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                          C.c_uint32, C.c_float, C.c_float, C.c_float, C.c_void_p]
+        L.dlk_grammar_mode_of.restype = C.c_int
+        L.dlk_grammar_mode_of.argtypes = [C.c_char_p]
+        L.dlk_grammar_row_init.argtypes = [C.POINTER(GrammarRow), C.c_int]
+        L.dlk_grammar_row_feed.argtypes = [C.POINTER(GrammarRow), C.c_char_p, C.c_int]
+        L.dlk_grammar_mask.restype = C.c_int
+        L.dlk_grammar_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                       C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]
+        # include/sampler.h
+        L.sampler_create.restype = C.c_void_p
+        L.sampler_create.argtypes = [C.POINTER(SamplerConfig)]
+        L.sampler_free.argtypes = [C.c_void_p]
+        L.sampler_sample.restype = C.c_int
+        L.sampler_sample.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.greedy_sample.restype = C.c_int
+        L.greedy_sample.argtypes = [C.c_void_p, C.c_int]
+        for fn in ("sampler_apply_repetition_penalty", "sampler_apply_presence_penalty"):
+            getattr(L, fn).argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_float]
+        # include/grammar.h
+        for fn in ("diskllm_grammar_init_from_file", "diskllm_grammar_init_from_str"):
+            getattr(L, fn).restype = C.c_void_p
+            getattr(L, fn).argtypes = [C.c_char_p]
+        L.diskllm_grammar_init_json.restype = C.c_void_p
+        L.diskllm_grammar_init_json.argtypes = []
+        L.diskllm_grammar_free.argtypes = [C.c_void_p]
+        L.diskllm_grammar_reset.argtypes = [C.c_void_p]
+        L.diskllm_grammar_accept_str.restype = C.c_bool
+        L.diskllm_grammar_accept_str.argtypes = [C.c_void_p, C.c_char_p]
+        L.diskllm_grammar_advance.argtypes = [C.c_void_p, C.c_char_p]
+        L.diskllm_grammar_is_finished.restype = C.c_bool
+        L.diskllm_grammar_is_finished.argtypes = [C.c_void_p]
+        L.diskllm_grammar_apply_mask.restype = C.c_int
+        L.diskllm_grammar_apply_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         _LIB = L
     return _LIB
 

@@ -244,7 +244,6 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         if (t == T - 1) misc[0] = (int)base;
     }
     __syncthreads();
-    const int np = misc[0];
     for (int i = t; i < nh; i += T) {
         const int id = hl[i];
         if (id >= s0 && id < s1) atomicAdd(&L.pcnt[slice_rank(sbits, spre, id - s0)], 1);

@@ -1,0 +1,125 @@
+/*
+ * dropin_sampler.c -- include/sampler.h on the GPU: the reference's single-row
+ * host API (include/sampler.h:19-34, src/sampler.c) as copies around the
+ * batched entry points of diskllm_amd.h.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "diskllm_amd.h"
+#include "sampler.h"
+#include "dropin.h"
+
+struct sampler {
+    sampler_config cfg;
+    uint64_t rng;            /* host copy of the xorshift state (src/sampler.c:63) */
+    dlk_dropin_ctx dev;
+};
+
+sampler *sampler_create(const sampler_config *cfg) {
+    if (!cfg) return NULL;
+    sampler *s = calloc(1, sizeof(*s));
+    if (!s) return NULL;
+    s->cfg = *cfg;
+    s->rng = dlk_seed_state(cfg->seed);                      /* src/sampler.c:87 */
+    if (dlk_dropin_init(&s->dev) != 0) {
+        free(s);
+        return NULL;
+    }
+    return s;
+}
+
+void sampler_free(sampler *s) {
+    if (!s) return;
+    dlk_dropin_release(&s->dev);
+    free(s);
+}
+
+/* One row through dlk_sample on `c`; rng updated in place when not greedy. */
+static int sample_one(dlk_dropin_ctx *c, const float *logits, int vocab, float temperature, int top_k, float top_p,
+                      float min_p, uint64_t *rng) {
+    if (dlk_dropin_reserve(c, vocab, 0) != 0) return -1;
+    const int greedy = temperature == 0.0f;
+    if (hipMemcpyAsync(c->logits, logits, (size_t)vocab * sizeof(float), hipMemcpyHostToDevice, c->stream) !=
+        hipSuccess)
+        return -1;
+    if (!greedy &&
+        hipMemcpyAsync(c->rng, rng, sizeof(uint64_t), hipMemcpyHostToDevice, c->stream) != hipSuccess)
+        return -1;
+    dlk_batch b;
+    memset(&b, 0, sizeof(b));
+    b.logits = c->logits;
+    b.ld = vocab;
+    b.rng = c->rng;
+    b.out_ids = c->ids;
+    b.status = c->status;
+    dlk_sample_params p;
+    memset(&p, 0, sizeof(p));
+    p.temperature = temperature;
+    p.top_k = top_k;
+    p.top_p = top_p;
+    p.min_p = min_p;
+    p.repeat_penalty = 1.0f;
+    if (hipMemsetAsync(c->status, 0, sizeof(uint32_t), c->stream) != hipSuccess) return -1;
+    if (dlk_sample(&b, 1, vocab, &p, c->stream) != DLK_OK) return -1;
+    int32_t id = -1;
+    uint32_t st = 0;
+    if (hipMemcpyAsync(&id, c->ids, sizeof(int32_t), hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
+    if (hipMemcpyAsync(&st, c->status, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
+    uint64_t r = 0;
+    if (!greedy && hipMemcpyAsync(&r, c->rng, sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+        return -1;
+    if (hipStreamSynchronize(c->stream) != hipSuccess || st != 0) return -1;
+    if (!greedy) *rng = r;
+    return id;
+}
+
+int sampler_sample(sampler *s, float *logits, int vocab_size) {
+    if (!s || !logits || vocab_size <= 0) return -1;
+    return sample_one(&s->dev, logits, vocab_size, s->cfg.temperature, s->cfg.top_k, s->cfg.top_p, s->cfg.min_p,
+                      &s->rng);
+}
+
+int greedy_sample(const float *logits, int vocab_size) {
+    if (!logits || vocab_size <= 0) return 0;
+    dlk_dropin_ctx *c = dlk_dropin_shared_lock();
+    if (!c) return -1;
+    uint64_t unused = 1;
+    const int id = sample_one(c, logits, vocab_size, 0.0f, 0, 1.0f, 0.0f, &unused);
+    dlk_dropin_shared_unlock();
+    return id;
+}
+
+/* One penalty op in place on the host row (ids outside [0, vocab) are skipped
+ * on the device, as the reference skips them). */
+static void penalty_one(float *logits, int vocab, const int *seen, int n, uint32_t op, float value) {
+    dlk_dropin_ctx *c = dlk_dropin_shared_lock();
+    if (!c) return;
+    if (dlk_dropin_reserve(c, vocab, n) == 0) {
+        const int32_t hoff[2] = {0, n};
+        const size_t bytes = (size_t)vocab * sizeof(float);
+        int ok = hipMemcpyAsync(c->logits, logits, bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+                 hipMemcpyAsync(c->hist, seen, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream) ==
+                     hipSuccess &&
+                 hipMemcpyAsync(c->hoff, hoff, sizeof(hoff), hipMemcpyHostToDevice, c->stream) == hipSuccess;
+        if (ok)
+            ok = dlk_apply_penalties(c->logits, vocab, 1, vocab, c->hoff, c->hist, op,
+                                     op == DLK_OP_REPETITION ? value : 1.0f, 0.0f,
+                                     op == DLK_OP_PRESENCE ? value : 0.0f, c->stream) == DLK_OK;
+        if (ok) hipMemcpyAsync(logits, c->logits, bytes, hipMemcpyDeviceToHost, c->stream);
+        hipStreamSynchronize(c->stream);
+    }
+    dlk_dropin_shared_unlock();
+}
+
+void sampler_apply_repetition_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,
+                                      float penalty) {
+    if (penalty <= 1.0f || !seen_tokens || num_seen <= 0 || !logits || vocab_size <= 0) return;   /* :22 */
+    penalty_one(logits, vocab_size, seen_tokens, num_seen, DLK_OP_REPETITION, penalty);
+}
+
+void sampler_apply_presence_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,
+                                    float presence_penalty) {
+    if (presence_penalty == 0.0f || !seen_tokens || num_seen <= 0 || !logits || vocab_size <= 0) return;  /* :36 */
+    penalty_one(logits, vocab_size, seen_tokens, num_seen, DLK_OP_PRESENCE, presence_penalty);
+}

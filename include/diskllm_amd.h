@@ -102,6 +102,70 @@ int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const uin
  * reference's softmax calls (src/sampler.c:179; glibc 2.35, x86-64 FMA variant). */
 int dlk_expf(const float *x, float *y, int64_t n, hipStream_t stream);
 
+/* Penalties in place on device logits [rows, ld], history as in dlk_batch
+ * (hist_off [rows+1], hist_ids).  One call replaces, per row,
+ * sampler_apply_presence_penalty (src/sampler.c:35-52: `pres` subtracted once
+ * per distinct in-range id) and sampler_apply_repetition_penalty (:21-33: once
+ * per occurrence, negative logits multiplied, others divided, only when
+ * rep > 1), plus the frequency penalty (freq * count once per distinct id), in
+ * `order` (DLK_OP_* nibbles, low first). */
+int dlk_apply_penalties(float *logits, int64_t ld, int rows, int vocab, const int32_t *hist_off,
+                        const int32_t *hist_ids, uint32_t order, float rep, float freq, float pres,
+                        hipStream_t stream);
+
+/* ---- grammar masks (src/core/grammar.c) ------------------------------------ */
+
+/* Grammar modes, chosen from the grammar text as diskllm_grammar_init_from_str
+ * does (src/core/grammar.c:21-26): receipt when it names bbox_2d (checked
+ * first, :240), else JSON when it names object or value, else no constraint. */
+#define DLK_GRAMMAR_NONE 0
+#define DLK_GRAMMAR_JSON 1
+#define DLK_GRAMMAR_RECEIPT 2
+#define DLK_GRAMMAR_BUF 8192      /* the reference's buffer: buffer + piece must stay < 8191 bytes */
+
+/* State of one validator after the bytes fed so far (a resumable form of
+ * is_valid_receipt_prefix / is_valid_json_prefix, src/core/grammar.c:68-226). */
+typedef struct {
+    int32_t mode;             /* DLK_GRAMMAR_* */
+    int32_t pc;               /* program point; 255 = rejected */
+    int32_t n, m;             /* receipt: key / number position; JSON: brace / bracket depth */
+    uint8_t prev;             /* previous byte */
+    uint8_t flag;             /* receipt: the number had a digit; JSON: inside a string */
+    uint8_t pad[2];
+} dlk_scan_state;
+
+/* Balance of the whole buffer (diskllm_grammar_is_finished, src/core/grammar.c:258-273). */
+typedef struct {
+    int32_t braces, brackets;
+    int32_t len;              /* bytes in the buffer */
+    uint8_t in_str, prev, pad[2];
+} dlk_balance_state;
+
+/* One sequence's grammar position: everything the mask needs about its buffer. */
+typedef struct {
+    dlk_scan_state scan;
+    dlk_balance_state bal;
+} dlk_grammar_row;
+
+/* Host helpers (plain C, no device work): the mode a grammar text selects, a
+ * fresh row, and a row advanced by n appended buffer bytes. */
+int dlk_grammar_mode_of(const char *grammar_text);
+void dlk_grammar_row_init(dlk_grammar_row *row, int mode);
+void dlk_grammar_row_feed(dlk_grammar_row *row, const char *bytes, int n);
+
+/* Grammar allow-masks for `rows` sequences (states: device array of
+ * dlk_grammar_row) over one vocabulary of token strings in CSR form, token t =
+ * bytes[off[t] .. off[t+1]) read up to its first NUL (strlen).  Per token, as
+ * diskllm_grammar_apply_mask (src/core/grammar.c:275-308): the EOS id is
+ * allowed iff the buffer is finished; an empty string is not allowed; any other
+ * token iff buffer + token fits the buffer and is still a valid prefix.
+ * Writes mask[r * mask_ld + w] (bit t%32 of word t/32, 1 = allowed); when
+ * `logits` is not NULL sets disallowed logits[r * ld + t] to -inf; when `valid`
+ * is not NULL writes each row's allowed count (the reference's return value). */
+int dlk_grammar_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const dlk_grammar_row *states,
+                     int rows, int eos_id, uint32_t *mask, int64_t mask_ld, float *logits, int64_t ld,
+                     int32_t *valid, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

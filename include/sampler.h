@@ -1,0 +1,61 @@
+/*
+ * sampler.h -- drop-in for DiskLLM's include/sampler.h (same types, names and
+ * signatures; include/sampler.h:7-34 of the reference), implemented by
+ * libdiskllm_amd.so on the GPU: every call copies the caller's host row to the
+ * device, runs the batched kernels of diskllm_amd.h on one row and copies the
+ * result back.  Results are bit-identical to the reference built as strict ISO C.
+ *
+ * Each sampler owns a HIP stream and device buffers; like the reference's it is
+ * not thread-safe.  greedy_sample and the two penalty functions take no sampler
+ * and share one lazily created per-process context guarded by a mutex.
+ */
+#ifndef SAMPLER_H
+#define SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque sampler state (reference: src/sampler.c:61-66). */
+typedef struct sampler sampler;
+
+/* Sampling configuration (reference include/sampler.h:10-16). */
+typedef struct {
+    float temperature;   /* 0 = greedy; otherwise logits are scaled by 1/temperature */
+    int top_k;           /* 0 (or >= vocab) = no top-k */
+    float top_p;         /* >= 1 = no nucleus cut */
+    float min_p;         /* <= 0 = no min-p cut (absolute probability threshold) */
+    uint64_t seed;       /* xorshift64 seed; 0 selects 0xDEADBEEF12345678 */
+} sampler_config;
+
+/* A sampler with its own rng state; NULL on failure (no GPU, no memory). */
+sampler *sampler_create(const sampler_config *cfg);
+
+void sampler_free(sampler *s);
+
+/* In place on the host row: once per occurrence, negative logits multiplied by
+ * `penalty`, others divided; nothing unless penalty > 1 (src/sampler.c:21-33). */
+void sampler_apply_repetition_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,
+                                      float penalty);
+
+/* In place on the host row: presence_penalty subtracted once per distinct
+ * seen id (src/sampler.c:35-52). */
+void sampler_apply_presence_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,
+                                    float presence_penalty);
+
+/* One token from the row (src/sampler.c:136-234); advances the rng state once
+ * unless temperature == 0.  The row is not modified.  Returns -1 only when the
+ * device call fails or the configuration is outside what the device path
+ * implements (a negative or denormal-small temperature). */
+int sampler_sample(sampler *s, float *logits, int vocab_size);
+
+/* First index of the maximum; 0 when logits[0] is NaN (src/sampler.c:9-19). */
+int greedy_sample(const float *logits, int vocab_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -39,6 +39,10 @@ class OrcTrace(C.Structure):
                 ("sum", C.c_double), ("s2", C.c_double), ("s3", C.c_double)]
 
 
+class OrcGrammar(C.Structure):
+    _fields_ = [("buf", C.c_char * 8192), ("len", C.c_int), ("is_json", C.c_bool), ("is_receipt", C.c_bool)]
+
+
 class SamplerConfig(C.Structure):
     """include/sampler.h:10-16."""
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
@@ -79,6 +83,13 @@ def lib() -> C.CDLL:
         L.orc_json_prefix.restype = C.c_bool
         L.orc_json_prefix.argtypes = [C.c_char_p, C.c_int]
         L.orc_expf_bits.argtypes = [C.c_uint32, C.c_long, _f32p, C.c_int]
+        L.orc_grammar_init.argtypes = [C.POINTER(OrcGrammar), C.c_char_p]
+        L.orc_grammar_accept.restype = C.c_bool
+        L.orc_grammar_accept.argtypes = [C.POINTER(OrcGrammar), C.c_char_p]
+        L.orc_grammar_advance.argtypes = [C.POINTER(OrcGrammar), C.c_char_p]
+        L.orc_grammar_finished.restype = C.c_bool
+        L.orc_grammar_finished.argtypes = [C.POINTER(OrcGrammar)]
+        L.orc_grammar_mask.argtypes = [C.POINTER(OrcGrammar), _f32p, C.c_int, _u32p, _u8p, C.c_int]
         _LIB = L
     return _LIB
 
@@ -109,6 +120,7 @@ def ref(kind: str = "strict") -> Optional[C.CDLL]:
         L.diskllm_grammar_advance.argtypes = [C.c_void_p, C.c_char_p]
         L.diskllm_grammar_is_finished.restype = C.c_bool
         L.diskllm_grammar_is_finished.argtypes = [C.c_void_p]
+        L.diskllm_grammar_apply_mask.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         _REFS[kind] = L
     return _REFS[kind]
 
@@ -213,3 +225,21 @@ def ref_sample_row(kind: str, row: np.ndarray, state: int, temperature: float, t
     work = np.ascontiguousarray(row, np.float32).copy()
     tok = L.refh_sample_trace(C.byref(cfg), C.byref(s), work, work.size, n_trace, oi, ov)
     return int(tok), int(s.value), oi[:n_trace], ov[:n_trace]
+
+
+# ------------------------------------------------------------------------- grammar
+
+def grammar(text: Optional[bytes]) -> OrcGrammar:
+    g = OrcGrammar()
+    lib().orc_grammar_init(C.byref(g), text)
+    return g
+
+
+def grammar_mask(g: OrcGrammar, offsets: np.ndarray, data: np.ndarray, eos_id: int,
+                 logits: Optional[np.ndarray] = None) -> tuple[np.ndarray, int]:
+    """orc_grammar_mask over a CSR vocabulary: the masked logits and the valid count."""
+    V = len(offsets) - 1
+    lg = np.zeros(V, np.float32) if logits is None else np.ascontiguousarray(logits, np.float32).copy()
+    n = lib().orc_grammar_mask(C.byref(g), lg, V, np.ascontiguousarray(offsets, np.uint32),
+                               np.ascontiguousarray(data, np.uint8), int(eos_id))
+    return lg, int(n)
