@@ -437,6 +437,124 @@ __device__ __forceinline__ ResolveOut<MB> exact_sum(int n, const QF &q, const Ag
 
 /* The reference's softmax/min-p/top-p/draw over n candidate positions.
  * Returns the sampled position; fills S. */
+/* ------------------------------------------------- rows holding NaN or +inf */
+
+/* Top-k rows holding NaN or +inf after the mask and penalties: once NaN takes
+ * part, the reference's insertion sort keeps NaN entries in place and stops
+ * other entries at them, and its sums and comparisons turn NaN, so the outcome
+ * depends on the order of every step.  One thread therefore runs the
+ * reference's own sequence (src/sampler.c:155-233): the row max (:155-158),
+ * s = (l - max) * (1/T) (:160-162), the insertion partial sort (:109-134), the
+ * softmax over the k candidates (:173-185), min-p (:188-202), top-p (:205-222)
+ * and the draw (:225-233).  cand holds k (value bits << 32 | index) entries.
+ * Writes the token and the candidate outputs; call from thread 0 only. */
+__device__ __forceinline__ void emulate_topk_row(const RowParams &p, const Row &R, int k, float r, uint64_t *cand,
+                                                 int row) {
+    auto ent = [](int i, float v) { return ((uint64_t)f2u(v) << 32) | (uint32_t)i; };
+    auto val = [](uint64_t e) { return u2f((uint32_t)(e >> 32)); };
+    const int V = R.V;
+    float mx = prepared(R, 0);
+    for (int i = 1; i < V; i++) {
+        const float x = prepared(R, i);
+        if (x > mx) mx = x;
+    }
+    const float inv_t = R.inv_t;
+    for (int i = 0; i < k; i++) cand[i] = ent(i, (prepared(R, i) - mx) * inv_t);
+    for (int i = 1; i < k; i++) {
+        const uint64_t tmp = cand[i];
+        int j = i;
+        while (j > 0 && val(cand[j - 1]) < val(tmp)) { cand[j] = cand[j - 1]; j--; }
+        cand[j] = tmp;
+    }
+    for (int i = k; i < V; i++) {
+        const float v = (prepared(R, i) - mx) * inv_t;
+        if (v > val(cand[k - 1])) {
+            const uint64_t tmp = ent(i, v);
+            int j = k - 1;
+            while (j > 0 && val(cand[j - 1]) < v) { cand[j] = cand[j - 1]; j--; }
+            cand[j] = tmp;
+        }
+    }
+    /* softmax over the k candidates */
+    float mv = val(cand[0]);
+    for (int i = 1; i < k; i++)
+        if (val(cand[i]) > mv) mv = val(cand[i]);
+    double sum = 0.0;
+    for (int i = 0; i < k; i++) {
+        const float e = dlk_expf_glibc(val(cand[i]) - mv, R.tab);
+        cand[i] = ent((int)(uint32_t)cand[i], e);
+        sum += e;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int i = 0; i < k; i++) cand[i] = ent((int)(uint32_t)cand[i], val(cand[i]) * inv);
+    /* min-p: the list is the entries >= min_p when any is, else all k */
+    const bool minp = p.min_p > 0.0f;
+    int nmin = 0;
+    if (minp)
+        for (int i = 0; i < k; i++) nmin += val(cand[i]) >= p.min_p;
+    const bool all = !minp || nmin == 0;
+    auto member = [&](int i) { return all || val(cand[i]) >= p.min_p; };
+    float inv2 = 1.0f;
+    if (minp) {
+        double s2 = 0.0;
+        for (int i = 0; i < k; i++)
+            if (member(i)) s2 += val(cand[i]);
+        inv2 = (float)(1.0 / s2);
+    }
+    auto w = [&](int i) { return minp ? val(cand[i]) * inv2 : val(cand[i]); };
+    /* top-p over the list: nk members kept */
+    int nk = all ? k : nmin;
+    float inv3 = 1.0f;
+    const bool topp = p.top_p < 1.0f;
+    if (topp) {
+        double cum = 0.0;
+        int rank = 0;
+        for (int i = 0; i < k; i++) {
+            if (!member(i)) continue;
+            cum += w(i);
+            rank++;
+            if ((float)cum >= p.top_p) { nk = rank; break; }
+        }
+        double s3 = 0.0;
+        rank = 0;
+        for (int i = 0; i < k && rank < nk; i++) {
+            if (!member(i)) continue;
+            s3 += w(i);
+            rank++;
+        }
+        inv3 = (float)(1.0 / s3);
+    }
+    auto q = [&](int i) { return topp ? w(i) * inv3 : w(i); };
+    /* the draw */
+    float cum = 0.0f;
+    int tok = -1, last = -1, rank = 0;
+    for (int i = 0; i < k && rank < nk; i++) {
+        if (!member(i)) continue;
+        cum += q(i);
+        rank++;
+        last = (int)(uint32_t)cand[i];
+        if (r < cum) { tok = last; break; }
+    }
+    p.out_ids[row] = tok >= 0 ? tok : last;
+    /* candidate outputs: softmax probabilities and log of the final ones */
+    rank = 0;
+    for (int j = 0; j < p.n_out; j++) {
+        const int64_t o = (int64_t)row * p.n_out + j;
+        if (j < k) {
+            const bool in = member(j) && rank < nk;
+            if (member(j)) rank++;
+            const float fj = in ? q(j) : 0.0f;
+            if (p.out_cand_ids) p.out_cand_ids[o] = (int)(uint32_t)cand[j];
+            if (p.out_cand_probs) p.out_cand_probs[o] = val(cand[j]);
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
+        } else {
+            if (p.out_cand_ids) p.out_cand_ids[o] = -1;
+            if (p.out_cand_probs) p.out_cand_probs[o] = 0.0f;
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = -INFINITY;
+        }
+    }
+}
+
 template <class B>
 __device__ __forceinline__ int pipeline(const RowParams &p, const B &base, int n, float r, unsigned char *region, Lds &L, Scal &S) {
     Aggs A = make_aggs(region, n);

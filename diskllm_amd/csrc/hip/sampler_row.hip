@@ -41,11 +41,14 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
     /* max / argmax over the prepared row (src/sampler.c:9-19, :155-158) */
     float bv = -INFINITY;
     int bidx = 0x7fffffff;
+    int irr = 0;                                  /* NaN or +inf after the mask and penalties */
     for (int i = t; i < V; i += blockDim.x) {
         float x = prepared(R, i);
         if (x > bv || (x == bv && i < bidx)) { bv = x; bidx = i; }
+        irr |= !(x < INFINITY) && !(x == -INFINITY);
     }
     block_argmax(bv, bidx, L);
+    irr = block_sum_int(irr, L);
     const bool first_nan = isnan(prepared(R, 0));
 
     const int n_out = p.n_out;
@@ -65,7 +68,14 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
     if (t == 0) p.rng[row] = st;
 
     const int k = p.topk_on ? p.top_k : V;
-    if (!(bv > -INFINITY)) {
+    if (irr && p.topk_on) {
+        if (t == 0) emulate_topk_row(p, R, k, r, (uint64_t *)L.region, row);
+        return;
+    }
+    if (irr || !(bv > -INFINITY)) {
+        /* without top-k a NaN or +inf entry makes the softmax sum NaN (+inf - max
+         * is NaN): as for a row of -inf, no comparison with it holds and the draw
+         * falls through to the last candidate */
         /* every entry -inf: the softmax is NaN throughout and the draw falls
          * through to the last candidate, which is index k-1 in index order */
         if (t == 0) p.out_ids[row] = k - 1;

@@ -18,7 +18,7 @@ struct TopkSlot {
     uint32_t kept;       /* candidates published */
     uint32_t complete;   /* 1: every finite entry published; 0: partial; 0xffffffff: overflow */
     uint32_t last_key;   /* desc key of the last published candidate */
-    uint32_t first_nan;  /* slice 0 only: prepared logit 0 is NaN (greedy rule) */
+    uint32_t first_nan;  /* bit 0 (slice 0): prepared logit 0 is NaN; bit 1: NaN or +inf in the slice */
     uint32_t pad;
 };
 

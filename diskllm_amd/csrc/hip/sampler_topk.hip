@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     /* ---- 2. stream the slice into registers ---------------------------- */
     float v[EPT];
     float tm = -INFINITY;
-    int targ = 0x7fffffff, nfin = 0;
+    int targ = 0x7fffffff, nfin = 0, irr = 0;
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int i0 = s0 + 4 * (t + j4 * T);
@@ -149,6 +149,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
             if (i < s1) {
                 if (x > tm || (x == tm && i < targ)) { tm = x; targ = i; }
                 nfin += (x > -INFINITY);
+                irr |= !(x < INFINITY) && !(x == -INFINITY);
             }
         }
     }
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     int bi = targ;
     block_argmax(bm, bi, L);
     int nf = block_sum_int(nfin, L);
+    irr = block_sum_int(irr, L);
     TopkSlot *slot = f.slots + ((int64_t)row * G + g);
     uint64_t *cands = f.cands + ((int64_t)row * G + g) * f.KP;
 
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         pub32(&slot->kept, (uint32_t)kept);
         pub32(&slot->complete, (uint32_t)complete);
         pub32(&slot->last_key, last_key);
-        pub32(&slot->first_nan, (g == 0 && isnan(v[0])) ? 1u : 0u);
+        pub32(&slot->first_nan, ((g == 0 && isnan(v[0])) ? 1u : 0u) | (irr ? 2u : 0u));
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     /* slot h -> LDS (misc[16..]: kept, complete, last_key per slice; up to 64 slices per pass) */
     uint32_t *sk = (uint32_t *)tmax;                 /* tmax is free now: 3 words per slice */
     float M = -INFINITY;
-    int amax = 0x7fffffff, NF = 0, total = 0, overflow = 0, first_nan = 0;
+    int amax = 0x7fffffff, NF = 0, total = 0, overflow = 0, first_nan = 0, irregular = 0;
     for (int h = t; h < G; h += T) {
         TopkSlot *s = f.slots + ((int64_t)row * G + h);
         sk[3 * h + 0] = get32(&s->kept);
@@ -241,7 +243,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         int a = (int)(uint32_t)buf[h];
         if (m > M || (m == M && a < amax)) { M = m; amax = a; }
         NF += (int)(buf[G + h] >> 32);
-        first_nan |= (int)(uint32_t)buf[G + h];
+        first_nan |= (int)((uint32_t)buf[G + h] & 1u);
+        irregular |= (int)((uint32_t)buf[G + h] & 2u);
         total += (int)sk[3 * h];
         overflow |= (int)sk[3 * h + 1] == -1;
     }
@@ -265,6 +268,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     __syncthreads();
     if (t == 0) p.rng[row] = st;
     const int k = p.top_k;
+    if (irregular) {
+        /* NaN or +inf in the row: the reference's sequence on one thread */
+        Row R;
+        R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.pflag = L.pflag;
+        R.M = 0.0f; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab;
+        R.np = build_patches(p, row, lg, mk, L, p.plan, V);
+        if (t == 0) emulate_topk_row(p, R, k, r, buf, row);
+        return;
+    }
     if (NF == 0) {                           /* every entry -inf (see sampler_row.hip) */
         if (t == 0) p.out_ids[row] = k - 1;
         out_cands_empty(NAN, NAN, true, k);

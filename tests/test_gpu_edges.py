@@ -163,3 +163,26 @@ def test_full_vocab_many_rows(cuda, path):
     """More rows than one cooperative launch holds: the host splits the batch."""
     w = W.c2(seed=41, rows=300, vocab=16384)
     run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", [0, 1, 2])
+def test_nan_and_inf_rows(cuda, path):
+    """NaN / +inf logits make the reference's softmax sum NaN: every comparison
+    after it fails and the draw falls through (src/sampler.c:226-233)."""
+    for V, k, tp, mp in ((20000, 0, 0.9, 0.0), (20000, 0, 1.0, 0.0), (9000, 7, 0.95, 0.0), (9000, 50, 0.9, 0.01),
+                         (300, 20, 1.0, 0.0)):
+        if path == 2 and k:
+            continue
+        rows = 6
+        lg = np.random.default_rng(V + k).normal(0, 2, size=(rows, V)).astype(np.float32)
+        lg[0, 0] = np.nan
+        lg[1, V // 2] = np.nan
+        lg[2, V - 1] = np.inf
+        lg[3, 1] = np.inf
+        lg[3, 2] = np.nan
+        lg[4, :] = -np.inf
+        lg[4, V // 3] = np.inf
+        lg[5, 3] = np.nan                            # NaN late in the first k: a barrier for the insertion sort
+        w = make(f"nan-inf-k{k}-p{tp}-mp{mp}", rows, V, seed=5, temperature=1.0, top_k=k, top_p=tp, min_p=mp,
+                 logits=lg, n_out=12)
+        run_and_check(w, path)

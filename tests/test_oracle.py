@@ -417,3 +417,30 @@ def test_expf_restatement_vs_host_libm():
                            timeout=300)
         checked, bad = map(int, r.stdout.split())
         assert checked > 500000 and bad == 0, (mode, r.stdout, r.stderr[:500])
+
+
+@needs_ref
+def test_sample_nan_and_inf_rows_vs_reference():
+    """NaN and +inf logits (the softmax sum turns NaN and no comparison holds):
+    the restatement follows the reference there too, with and without top-k."""
+    rng = np.random.default_rng(13)
+    for V in (5, 300, 20000):
+        for (T, k, p) in ((1.0, 0, 0.9), (0.8, 4, 0.95), (1.0, 0, 1.0)):
+            for case in range(5):
+                row = rng.normal(0, 2, V).astype(np.float32)
+                if case == 0:
+                    row[0] = np.nan
+                elif case == 1:
+                    row[V // 2] = np.nan
+                elif case == 2:
+                    row[V - 1] = np.inf
+                elif case == 3:
+                    row[1] = np.inf
+                    row[2] = np.nan
+                else:
+                    row[:] = -np.inf
+                    row[V // 3] = np.inf
+                st = int(rng.integers(1, 2 ** 63))
+                tok, st_ref, _, _ = O.ref_sample_row("strict", row, st, T, k, p, 0.0)
+                o = O.sample_row(row, st, T, k, p, 0.0)
+                assert (o["token"], o["state"]) == (tok, st_ref), (V, T, k, p, case, o["token"], tok)
