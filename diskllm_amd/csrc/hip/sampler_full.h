@@ -22,7 +22,8 @@ enum : int {
     kSyncExit = 3,     /* workgroups finished */
     kSyncDone = 4,     /* token written */
     kSyncChain = 16,   /* + w: running value for workgroup w is ready */
-    kSyncChainVal = 32 /* + w: that running value (float bits) */
+    kSyncChainVal = 32,/* + w: that running value (float bits) */
+    kSyncWalk = 48     /* + w: walk data of slice w published for workgroup 0 */
 };
 
 /* published words per workgroup */
@@ -34,6 +35,7 @@ enum : int {
     kPubCandChunk = 4, /* + s: global chunk index */
     kPubCandPre = 6,   /* + s: double, slice-local exclusive p prefix at that chunk */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
+    kPubStaged = 9,    /* staged chunks in the published walk data */
 };
 
 struct FullParams {
@@ -41,9 +43,14 @@ struct FullParams {
     int G;             /* workgroups per row */
     int S;             /* slice length = EPT * kFullThreads */
     int stage_cap;     /* chunks of final probabilities kept in LDS per workgroup */
+    int pf_slices;     /* later slices whose walk data workgroup 0 prefetches into LDS */
+    int pf_cap;        /* staged chunks of a prefetched slice that fit its buffer */
     uint32_t *sync;    /* [rows][kSyncWords] */
     uint64_t *pub;     /* [rows][G][kPubWords] */
     float *cvals;      /* [rows][G][kCandSlots][64] */
+    uint4 *wruns;      /* [rows][G][nch]: per chunk {binade, next chunk, run total lo, hi} */
+    int *wsmap;        /* [rows][G][nch]: staged slot of each chunk or -1 */
+    float *wsvals;     /* [rows][G][stage_cap * 64]: staged chunks */
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;
     int force_exact;   /* test hook: send every row through the exact fallback */

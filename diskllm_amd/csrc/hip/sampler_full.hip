@@ -141,9 +141,11 @@ struct QSlice {
     int s0, x, topp;
     float M, inv_t, inv, inv3;
     const uint64_t *tab;
+    int *fail;         /* another workgroup's slice: only its staged chunks are here */
     DLK_DEV float operator()(int i) const {
         int sl = smap[i >> 6];
         if (sl >= 0) return svals[sl * 64 + (i & 63)];
+        if (fail) { *fail = 1; return 0.0f; }
         const int gi = s0 + i;
         if (gi > x) return 0.0f;
         float l = lg[gi];
@@ -190,22 +192,21 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     uint64_t *pc = (uint64_t *)carve(q, (size_t)G * kPubWords * 8);   /* published words, cached */
     int *misc = (int *)carve(q, 64 * 4);
     double *md = (double *)carve(q, 16 * 8);
+    /* workgroup 0: walk data of later slices, prefetched while it walks its own */
+    const int npf = g == 0 ? f.pf_slices : 0;
+    int *pf_bh = (int *)carve(q, (size_t)npf * nch * 4);
+    int *pf_next = (int *)carve(q, (size_t)npf * nch * 4);
+    uint64_t *pf_tot = (uint64_t *)carve(q, (size_t)npf * nch * 8);
+    int *pf_smap = (int *)carve(q, (size_t)npf * nch * 4);
+    float *pf_vals = (float *)carve(q, (size_t)npf * f.pf_cap * 64 * 4);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
     const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
     const float r = rand_f32_from(st);
 
-    /* ---- stream the slice into registers: every load issued before any use */
-    float4 raw[EPT / 4];
-    uint32_t mwd[EPT / 4];
-#pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        const int i0 = s0 + 4 * (t + j4 * T);
-        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
-        mwd[j4] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
-    }
-
-    /* ---- penalty patches of the ids inside this slice ------------------- */
+    /* ---- history first: each thread's id, and for an id inside this slice
+     *      its logit and mask word, gathered before the bulk loads so that
+     *      the penalties are computed while the slice is still in flight --- */
     const int32_t *hist = nullptr;
     int nh = 0;
     if (p.hist_off) {
@@ -220,14 +221,37 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         row_exit(sync, G);
         return;
     }
+    int hid = -1;
+    float gx = 0.0f;
+    uint32_t gm = 0xffffffffu;
+    if (t < nh) {
+        hid = hist[t];
+        if (hid >= s0 && hid < s1) {
+            gx = lg[hid];
+            if (mk) gm = mk[hid >> 5];
+        }
+    }
+
+    /* ---- stream the slice into registers: every load issued before any use */
+    float4 raw[EPT / 4];
+    uint32_t mwd[EPT / 4];
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
+        mwd[j4] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
+    }
+
+    /* ---- penalty patches of the ids inside this slice ------------------- */
     const int nw = S / 32;
+    int *pfirst = L.pid;                           /* first history position of each patched id */
     for (int i = t; i < nw; i += T) sbits[i] = 0;
-    for (int i = t; i < p.plan.hcap; i += T) L.pcnt[i] = 0;
+    for (int i = t; i < p.plan.hcap; i += T) { L.pcnt[i] = 0; pfirst[i] = 0x7fffffff; }
     if (t == 0) misc[5] = 0;
     __syncthreads();
     int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
     for (int i = t; i < nh; i += T) {
-        const int id = hist[i];
+        const int id = i == t ? hid : hist[i];
         hl[i] = id;
         if (id >= s0 && id < s1) atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
     }
@@ -241,12 +265,29 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         uint32_t base = block_excl_prefix_u32(cnt, (uint32_t *)L.bi);
         for (int k = 0; k < per; k++)
             if (w0 + k < nw) { spre[w0 + k] = base; base += __popc(sbits[w0 + k]); }
-        if (t == T - 1) misc[0] = (int)base;
     }
     __syncthreads();
     for (int i = t; i < nh; i += T) {
         const int id = hl[i];
-        if (id >= s0 && id < s1) atomicAdd(&L.pcnt[slice_rank(sbits, spre, id - s0)], 1);
+        if (id >= s0 && id < s1) {
+            const int slot = slice_rank(sbits, spre, id - s0);
+            atomicAdd(&L.pcnt[slot], 1);
+            atomicMin(&pfirst[slot], i);
+        }
+    }
+    __syncthreads();
+    /* the thread of an id's first occurrence applies its penalties (src/sampler.c:21-52) */
+    for (int i = t; i < nh; i += T) {
+        const int id = hl[i];
+        if (id < s0 || id >= s1) continue;
+        const int slot = slice_rank(sbits, spre, id - s0);
+        if (pfirst[slot] != i) continue;
+        float x;
+        uint32_t m;
+        if (i == t) { x = gx; m = gm; }
+        else { x = lg[id]; m = mk ? mk[id >> 5] : 0xffffffffu; }
+        if (!((m >> (id & 31)) & 1u)) x = -INFINITY;
+        L.pval[slot] = penalize(x, L.pcnt[slot], p);
     }
     __syncthreads();
 
@@ -269,11 +310,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             const int i = i0 + c;
             float x = xs[c];
             if (!((mw >> c) & 1u)) x = -INFINITY;
-            if ((pb >> c) & 1u) {
-                const int slot = slice_rank(sbits, spre, li0 + c);
-                x = penalize(x, L.pcnt[slot], p);
-                L.pval[slot] = x;
-            }
+            if ((pb >> c) & 1u) x = L.pval[slice_rank(sbits, spre, li0 + c)];
             if (i >= s1) x = -INFINITY;
             v[j4 * 4 + c] = x;
             tm = fmaxf(tm, x);
@@ -545,16 +582,20 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int c = u >> 4;
         int bh = predict_binade<24>(Pc[c]);
         bool valid = bh == predict_binade<24>(Pc[c + 1]) && bh >= -100;
-        uint32_t sum = 0;
+        /* the increments are integers below 2^24 wherever the prediction holds,
+         * so their float sum is exact; where it does not the sum still reaches
+         * 2^24 (non-negative terms, monotone rounding) and the walk opens the chunk */
+        float fsum = 0.0f;
         bool tie = false;
         if (valid) {
             for (int k = 0; k < 4; k++) {
-                float xs = ldexpf(v[4 * j4 + k], 23 - bh);
-                uint32_t n = xs >= 0x1p25f ? (1u << 25) : (uint32_t)rintf(xs);
-                tie |= xs < 0x1p24f && (xs - floorf(xs)) == 0.5f;
-                sum += n;
+                const float xs = ldexpf(v[4 * j4 + k], 23 - bh);
+                const float n = rintf(xs);
+                tie |= fabsf(xs - n) == 0.5f;
+                fsum += n;
             }
         }
+        uint32_t sum = (uint32_t)fminf(fsum, 0x1p25f);
         sum = row_scan_u32(sum);
         tie = ((ballot(tie) >> (lane & 48)) & 0xffffull) != 0;
         if ((lane & 15) == 15) {
@@ -608,7 +649,34 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     __syncthreads();
 
-    /* ---- chain: exact draw over this slice from the predecessor's value --- */
+    /* ---- walk data of the later slices, published for workgroup 0 ------- */
+    if (g > 0) {
+        const int64_t rg = (int64_t)row * G + g;
+        /* agent-scope stores: the reader may sit on another XCD, whose L2 is not
+         * coherent with this one for plain stores */
+        uint32_t *wr = (uint32_t *)(f.wruns + rg * nch);
+        uint32_t *wm = (uint32_t *)(f.wsmap + rg * nch);
+        uint32_t *wv = (uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
+        const int nst = min(misc[10], f.stage_cap);
+        for (int c = t; c < nch; c += T) {
+            at_st32(&wr[4 * c], (uint32_t)cbh[c]);
+            at_st32(&wr[4 * c + 1], (uint32_t)rnext[c]);
+            at_st32(&wr[4 * c + 2], (uint32_t)rtot[c]);
+            at_st32(&wr[4 * c + 3], (uint32_t)(rtot[c] >> 32));
+            at_st32(&wm[c], (uint32_t)smap[c]);
+        }
+        for (int i = t; i < nst * 64; i += T) at_st32(&wv[i], f2u(svals[i]));
+        if (t == 0) at_st64(&mypub[kPubStaged], (uint64_t)nst);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t == 0) at_st32(&sync[kSyncWalk + g], 1u);
+    }
+
+    /* ---- chain: exact draw, from the predecessor's exact value -------------
+     * Workgroup 0 walks its slice and then the later ones from their published
+     * walk data (no hand-off latency); a slice it cannot walk (an element-level
+     * chunk that was not staged) goes back to its owner, which walks it and
+     * hands on as the chain did before. */
     float c_in = 0.0f;
     if (g > 0) {
         if (t == 0) {
@@ -633,26 +701,120 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         c_in = u2f((uint32_t)misc[12]);
     }
-    const int n_loc = min(s1, x + 1) - s0;
-    QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, s0, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
-    if (wave_id() == 0) {
-        ResolveOut<24> o = resolve_runs(n_loc, qs, Runs{cbh, rtot, rnext}, vthr, c_in);
-        if (lane == 0) { misc[13] = o.pos; misc[14] = (int)f2u(o.value); }
-    }
-    __syncthreads();
-    const int pos = misc[13];
-    int token = -1;
-    if (pos >= 0) token = s0 + pos;
-    else if (x < s1) token = x;              /* nothing crossed r up to x: the last kept entry */
-    if (t == 0) {
+    int *fail = misc + 15;
+    int *pf_ok = misc + 32;                        /* [pf_slices]: slice prefetched */
+    for (int gw = g;; gw++) {
+        const int s0w = gw * S, s1w = min(V, s0w + S);
+        const bool own = gw == g;
+        const int k = gw - 1;                      /* prefetch slot of a later slice */
+        const bool pre = !own && k < npf && pf_ok[k];
+        int *w_bh = cbh, *w_next = rnext, *w_smap = smap;
+        uint64_t *w_tot = rtot;
+        float *w_vals = svals;
+        if (pre) {
+            w_bh = pf_bh + k * nch;
+            w_next = pf_next + k * nch;
+            w_tot = pf_tot + k * nch;
+            w_smap = pf_smap + k * nch;
+            w_vals = pf_vals + (int64_t)k * f.pf_cap * 64;
+        }
+        if (!own && !pre) {
+            /* slice gw's runs and staged chunks into this workgroup's arrays */
+            if (t == 0) {
+                uint32_t spins = 0, ok = 1;
+                while (!at_ld32(&sync[kSyncWalk + gw]))
+                    if (++spins > kSpinLimit) {
+                        if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
+                        ok = 0;
+                        break;
+                    }
+                misc[11] = (int)ok;
+            }
+            __syncthreads();
+            if (!misc[11]) break;
+            const int64_t rg = (int64_t)row * G + gw;
+            const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
+            const int *wm = f.wsmap + rg * nch;
+            for (int c = t; c < nch; c += T) {
+                cbh[c] = (int)at_ld32(&wr[4 * c]);
+                rnext[c] = (int)at_ld32(&wr[4 * c + 1]);
+                rtot[c] = (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
+                smap[c] = (int)at_ld32((const uint32_t *)&wm[c]);
+            }
+            const int nst = (int)at_ld64(&pubrow[gw * kPubWords + kPubStaged]);
+            const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
+            for (int i = t; i < nst * 64; i += T) svals[i] = u2f(at_ld32(&wv[i]));
+        }
+        if (t == 0) *fail = 0;
+        if (own && npf > 0 && t < 64)
+            for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
+        __syncthreads();
+        const int n_loc = min(s1w, x + 1) - s0w;
+        QSlice qs{w_smap, w_vals, lg, mk, sbits, spre, L.pval, s0w, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab,
+                  own ? nullptr : fail};
+        if (wave_id() == 0) {
+            ResolveOut<24> o = resolve_runs(n_loc, qs, Runs{w_bh, w_tot, w_next}, vthr, c_in);
+            if (lane == 0) { misc[13] = o.pos; misc[14] = (int)f2u(o.value); }
+        } else if (own && npf > 0) {
+            /* the other waves fetch the later slices' walk data meanwhile */
+            const int tt = t - 64, TT = T - 64;
+            for (int kk = 0; kk < npf; kk++) {
+                const int gs = kk + 1;
+                bool ok = true;
+                if (lane == 0) {
+                    uint32_t spins = 0;
+                    while (!at_ld32(&sync[kSyncWalk + gs]))
+                        if (++spins > kSpinLimit) { ok = false; break; }
+                }
+                ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
+                if (!ok) break;                    /* the walk will wait for it itself */
+                const int nst = (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]);
+                if (nst > f.pf_cap) continue;
+                const int64_t rg = (int64_t)row * G + gs;
+                const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
+                const int *wm = f.wsmap + rg * nch;
+                for (int c = tt; c < nch; c += TT) {
+                    pf_bh[kk * nch + c] = (int)at_ld32(&wr[4 * c]);
+                    pf_next[kk * nch + c] = (int)at_ld32(&wr[4 * c + 1]);
+                    pf_tot[kk * nch + c] = (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
+                    pf_smap[kk * nch + c] = (int)at_ld32((const uint32_t *)&wm[c]);
+                }
+                const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
+                for (int i = tt; i < nst * 64; i += TT) pf_vals[(int64_t)kk * f.pf_cap * 64 + i] = u2f(at_ld32(&wv[i]));
+                if (tt == 0) pf_ok[kk] = 1;
+            }
+        }
+        __syncthreads();
+        if (*fail) {
+            /* hand slice gw to its owner with its exact starting value */
+            if (t == 0) {
+                at_st32(&sync[kSyncChainVal + gw], f2u(c_in));
+                __builtin_amdgcn_s_waitcnt(0);
+                at_st32(&sync[kSyncChain + gw], 1u);
+            }
+            break;
+        }
+        const int pos = misc[13];
+        int token = -1;
+        if (pos >= 0) token = s0w + pos;
+        else if (x < s1w) token = x;             /* nothing crossed r up to x: the last kept entry */
         if (token >= 0) {
-            p.out_ids[row] = token;
-            __builtin_amdgcn_s_waitcnt(0);
-            at_st32(&sync[kSyncDone], 1u);
-        } else {
-            at_st32(&sync[kSyncChainVal + g + 1], (uint32_t)misc[14]);
-            __builtin_amdgcn_s_waitcnt(0);
-            at_st32(&sync[kSyncChain + g + 1], 1u);
+            if (t == 0) {
+                p.out_ids[row] = token;
+                __builtin_amdgcn_s_waitcnt(0);
+                at_st32(&sync[kSyncDone], 1u);
+            }
+            break;
+        }
+        c_in = u2f((uint32_t)misc[14]);
+        if (g != 0 || gw + 1 >= G) {
+            /* a later workgroup walked its own slice: hand on to the next */
+            if (gw + 1 < G && t == 0) {
+                at_st32(&sync[kSyncChainVal + gw + 1], f2u(c_in));
+                __builtin_amdgcn_s_waitcnt(0);
+                at_st32(&sync[kSyncChain + gw + 1], 1u);
+            }
+            break;
         }
     }
     row_exit(sync, G);
