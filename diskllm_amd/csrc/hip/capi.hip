@@ -163,7 +163,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     f.stage_cap = 160;
     f.force_exact = force_exact;
     /* carve order of full_kernel: sbits, spre, ce, cp, cbh, ca, rtot, rnext, rend, rpre, Pc, smap, svals, pc,
-     * misc, md */
+     * misc, md (then the prefetch buffers) */
     size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
                  4 * r16((size_t)nch * 4) + 2 * r16((size_t)nch * 8) + r16((size_t)(nch + 1) * 8) +
                  r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) + r16((size_t)G * kPubWords * 8) +

@@ -375,25 +375,44 @@ DLK_DEV float wave_serial_sum(float c, float q) {
     return y;
 }
 
-/* First position pos < n where the running float sum c0 + q(0) + ... + q(pos)
- * reaches thr_v, and the running value there; {-1, final value} if none.
+/* Exact state of a walk between chunks: next chunk j, running value join_f(b, m). */
+struct WalkState {
+    int j;
+    int b;
+    uint32_t m;
+};
+/* pos >= 0: the first position whose running value reaches the threshold, and
+ * that value; pos == -1: no position up to n (value = final running value);
+ * need >= 0: the walk stopped at chunk `need`, which is not staged. */
+struct WalkOut {
+    int pos;
+    float value;
+    int need;
+};
+
+DLK_DEV int sreadi(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+/* Walks the running float sum c + q(0) + ... from state st over n elements:
+ * runs are crossed with their integer totals, any other chunk is summed
+ * element by element from its staged values (svals[smap[j] * 64 ...]).
  * Elements past n in the last chunk and in run totals must be zero. */
-template <class QF>
-__device__ __forceinline__ ResolveOut<24> resolve_runs(int n, const QF &q, const Runs &R, double thr_v, float c0) {
+__device__ __forceinline__ WalkOut walk_runs(int n, const int *smap, const float *svals, const Runs R, double thr_v,
+                                             WalkState &st) {
     const int lane = lane_id();
     const int nch = (n + 63) >> 6;
-    int b;
-    uint64_t m;
-    split(c0, b, m);
-    uint64_t thr = ceil_div_pow2(thr_v, b - 23);
-    int j = 0;
+    const uint32_t top = 1u << 24;
+    int b = st.b, j = st.j;
+    uint32_t m = st.m;
+    uint64_t t64 = ceil_div_pow2(thr_v, b - 23);
+    uint32_t thr = t64 < (1ull << 25) ? (uint32_t)t64 : (1u << 25);
     while (j < nch) {
-        if (R.bh[j] == b) {
-            const uint64_t lim = thr < (1ull << 24) ? thr : (1ull << 24);
+        if (sreadi(R.bh[j]) == b) {
+            const uint32_t lim = thr < top ? thr : top;
             uint64_t tot = R.tot[j];
-            const int nx = R.next[j];
-            if (m + tot < lim) {
-                m += tot;
+            tot = ((uint64_t)(uint32_t)sreadi((int)(tot >> 32)) << 32) | (uint32_t)sreadi((int)(uint32_t)tot);
+            const int nx = sreadi(R.next[j]);
+            if ((uint64_t)m + tot < lim) {
+                m += (uint32_t)tot;
                 j = nx;
                 continue;
             }
@@ -402,29 +421,42 @@ __device__ __forceinline__ ResolveOut<24> resolve_runs(int n, const QF &q, const
                 const int k = j + lane;
                 const uint64_t tk = k < nx ? R.tot[k] : 0;
                 const uint64_t tk1 = k + 1 < nx ? R.tot[k + 1] : 0;
-                const int f = first_lane(ballot(k < nx && m + (tot - tk1) >= lim));
+                const int f = first_lane(ballot(k < nx && (uint64_t)m + (tot - tk1) >= lim));
                 if (f < 64) {
-                    m += tot - readlane64(tk, f);
+                    m += (uint32_t)(tot - readlane64(tk, f));
                     j += f;
                     break;
                 }
                 const uint64_t tn = readlane64(tk1, 63);
-                m += tot - tn;
+                m += (uint32_t)(tot - tn);
                 tot = tn;
                 j += 64;
             }
         }
+        const int sl = sreadi(smap[j]);
+        if (sl < 0) {
+            st.j = j;
+            st.b = b;
+            st.m = m;
+            return WalkOut{-1, 0.0f, j};
+        }
         const int base = j * 64;
         const int count = min(64, n - base);
-        const float qv = lane < count ? q(base + lane) : 0.0f;
+        const float qv = lane < count ? svals[sl * 64 + lane] : 0.0f;
         const float y = wave_serial_sum(join_f(b, m), qv);
         const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
-        if (f < count) return ResolveOut<24>{base + f, readlanef(y, f)};
-        split(readlanef(y, count - 1), b, m);
-        thr = ceil_div_pow2(thr_v, b - 23);
+        if (f < count) return WalkOut{base + f, readlanef(y, f), -1};
+        uint64_t m64;
+        split(readlanef(y, count - 1), b, m64);
+        m = (uint32_t)m64;
+        t64 = ceil_div_pow2(thr_v, b - 23);
+        thr = t64 < (1ull << 25) ? (uint32_t)t64 : (1u << 25);
         j++;
     }
-    return ResolveOut<24>{-1, join_f(b, m)};
+    st.j = j;
+    st.b = b;
+    st.m = m;
+    return WalkOut{-1, join_f(b, m), -1};
 }
 
 }  // namespace dlk

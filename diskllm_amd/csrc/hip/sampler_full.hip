@@ -141,11 +141,9 @@ struct QSlice {
     int s0, x, topp;
     float M, inv_t, inv, inv3;
     const uint64_t *tab;
-    int *fail;         /* another workgroup's slice: only its staged chunks are here */
     DLK_DEV float operator()(int i) const {
         int sl = smap[i >> 6];
         if (sl >= 0) return svals[sl * 64 + (i & 63)];
-        if (fail) { *fail = 1; return 0.0f; }
         const int gi = s0 + i;
         if (gi > x) return 0.0f;
         float l = lg[gi];
@@ -622,6 +620,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             rtot[c] = vld ? rpre[run] - (ainc - a) : 0;
         }
     }
+    __syncthreads();
     /* chunks the walk may have to open: mispredicted or near a binade edge,
      * near the draw threshold, holding x, or holding a tie */
     const double vthr = (double)u2f(f2u(r) + 1u);
@@ -635,7 +634,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int sl = -1;
         if (want && s0 + 64 * c < s1 && s0 + 64 * c <= x) {
             sl = atomicAdd(&misc[10], 1);
-            if (sl >= f.stage_cap) sl = -1;
+            if (sl >= f.stage_cap - 1) sl = -1;         /* the last slot is the walk's spare */
         }
         smap[c] = sl;
     }
@@ -657,7 +656,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         uint32_t *wr = (uint32_t *)(f.wruns + rg * nch);
         uint32_t *wm = (uint32_t *)(f.wsmap + rg * nch);
         uint32_t *wv = (uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
-        const int nst = min(misc[10], f.stage_cap);
+        const int nst = min(misc[10], f.stage_cap - 1);
         for (int c = t; c < nch; c += T) {
             at_st32(&wr[4 * c], (uint32_t)cbh[c]);
             at_st32(&wr[4 * c + 1], (uint32_t)rnext[c]);
@@ -701,7 +700,6 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         c_in = u2f((uint32_t)misc[12]);
     }
-    int *fail = misc + 15;
     int *pf_ok = misc + 32;                        /* [pf_slices]: slice prefetched */
     for (int gw = g;; gw++) {
         const int s0w = gw * S, s1w = min(V, s0w + S);
@@ -745,55 +743,84 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
             for (int i = t; i < nst * 64; i += T) svals[i] = u2f(at_ld32(&wv[i]));
         }
-        if (t == 0) *fail = 0;
         if (own && npf > 0 && t < 64)
             for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
         __syncthreads();
         const int n_loc = min(s1w, x + 1) - s0w;
-        QSlice qs{w_smap, w_vals, lg, mk, sbits, spre, L.pval, s0w, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab,
-                  own ? nullptr : fail};
-        if (wave_id() == 0) {
-            ResolveOut<24> o = resolve_runs(n_loc, qs, Runs{w_bh, w_tot, w_next}, vthr, c_in);
-            if (lane == 0) { misc[13] = o.pos; misc[14] = (int)f2u(o.value); }
-        } else if (own && npf > 0) {
-            /* the other waves fetch the later slices' walk data meanwhile */
-            const int tt = t - 64, TT = T - 64;
-            for (int kk = 0; kk < npf; kk++) {
-                const int gs = kk + 1;
-                bool ok = true;
+        WalkState st;
+        {
+            uint64_t m64;
+            split(c_in, st.b, m64);
+            st.m = (uint32_t)m64;
+            st.j = 0;
+        }
+        bool handed = false;
+        for (int round = 0;; round++) {
+            if (wave_id() == 0) {
+                const WalkOut o = walk_runs(n_loc, w_smap, w_vals, Runs{w_bh, w_tot, w_next}, vthr, st);
                 if (lane == 0) {
-                    uint32_t spins = 0;
-                    while (!at_ld32(&sync[kSyncWalk + gs]))
-                        if (++spins > kSpinLimit) { ok = false; break; }
+                    misc[13] = o.pos;
+                    misc[14] = (int)f2u(o.value);
+                    misc[15] = o.need;
                 }
-                ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
-                if (!ok) break;                    /* the walk will wait for it itself */
-                const int nst = (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]);
-                if (nst > f.pf_cap) continue;
-                const int64_t rg = (int64_t)row * G + gs;
-                const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
-                const int *wm = f.wsmap + rg * nch;
-                for (int c = tt; c < nch; c += TT) {
-                    pf_bh[kk * nch + c] = (int)at_ld32(&wr[4 * c]);
-                    pf_next[kk * nch + c] = (int)at_ld32(&wr[4 * c + 1]);
-                    pf_tot[kk * nch + c] = (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
-                    pf_smap[kk * nch + c] = (int)at_ld32((const uint32_t *)&wm[c]);
+            } else if (own && npf > 0 && round == 0) {
+                /* the other waves fetch the later slices' walk data meanwhile */
+                const int tt = t - 64, TT = T - 64;
+                for (int kk = 0; kk < npf; kk++) {
+                    const int gs = kk + 1;
+                    bool ok = true;
+                    if (lane == 0) {
+                        uint32_t spins = 0;
+                        while (!at_ld32(&sync[kSyncWalk + gs]))
+                            if (++spins > kSpinLimit) { ok = false; break; }
+                    }
+                    ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
+                    if (!ok) break;                /* the walk will wait for it itself */
+                    const int nst = (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]);
+                    if (nst > f.pf_cap) continue;
+                    const int64_t rg = (int64_t)row * G + gs;
+                    const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
+                    const int *wm = f.wsmap + rg * nch;
+                    for (int c = tt; c < nch; c += TT) {
+                        pf_bh[kk * nch + c] = (int)at_ld32(&wr[4 * c]);
+                        pf_next[kk * nch + c] = (int)at_ld32(&wr[4 * c + 1]);
+                        pf_tot[kk * nch + c] =
+                            (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
+                        pf_smap[kk * nch + c] = (int)at_ld32((const uint32_t *)&wm[c]);
+                    }
+                    const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
+                    for (int i = tt; i < nst * 64; i += TT)
+                        pf_vals[(int64_t)kk * f.pf_cap * 64 + i] = u2f(at_ld32(&wv[i]));
+                    if (tt == 0) pf_ok[kk] = 1;
                 }
-                const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
-                for (int i = tt; i < nst * 64; i += TT) pf_vals[(int64_t)kk * f.pf_cap * 64 + i] = u2f(at_ld32(&wv[i]));
-                if (tt == 0) pf_ok[kk] = 1;
             }
-        }
-        __syncthreads();
-        if (*fail) {
-            /* hand slice gw to its owner with its exact starting value */
-            if (t == 0) {
-                at_st32(&sync[kSyncChainVal + gw], f2u(c_in));
-                __builtin_amdgcn_s_waitcnt(0);
-                at_st32(&sync[kSyncChain + gw], 1u);
+            __syncthreads();
+            const int need = misc[15];
+            if (need < 0) break;
+            if (!own) {
+                /* a chunk of another slice that was not staged: hand the slice to
+                 * its owner with its exact starting value */
+                if (t == 0) {
+                    at_st32(&sync[kSyncChainVal + gw], f2u(c_in));
+                    __builtin_amdgcn_s_waitcnt(0);
+                    at_st32(&sync[kSyncChain + gw], 1u);
+                }
+                handed = true;
+                break;
             }
-            break;
+            /* stage the chunk into the spare slot and resume the walk there */
+            const int spare = f.stage_cap - 1;
+            if (t < 64) {
+                QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, s0w, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
+                const int i = need * 64 + t;
+                const float val = i < n_loc ? qs(i) : 0.0f;
+                svals[spare * 64 + t] = val;
+            }
+            __syncthreads();
+            if (t == 0) smap[need] = spare;
+            __syncthreads();
         }
+        if (handed) break;
         const int pos = misc[13];
         int token = -1;
         if (pos >= 0) token = s0w + pos;
