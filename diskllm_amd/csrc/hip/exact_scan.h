@@ -353,12 +353,20 @@ __device__ __forceinline__ ResolveOut<MB> resolve(int n, const QF &q, const Aggs
  * grid 2^(b-23); consecutive such chunks of one binade form a run, and for each
  * chunk the integer total from it to the end of its run is precomputed, so the
  * walk crosses a run in one step.  Every other chunk (binade change, halfway
- * case, misprediction) is summed element by element in float. */
-struct Runs {
-    const int *bh;          /* [nch] binade of the chunk, or kInvalidBinade */
-    const uint64_t *tot;    /* [nch] increments from the chunk to the end of its run */
-    const int *next;        /* [nch] first chunk after the run */
-};
+ * case, misprediction) is summed element by element in float.
+ *
+ * Each chunk has one 16-byte record, read by the walk in one LDS access:
+ *   x = (binade & 0xffff) | (staged slot << 16)   binade = kInvalidBinade for an
+ *                                                  element-level chunk, slot -1
+ *                                                  when the values are not staged
+ *   y = first chunk after the chunk's run
+ *   z, w = low / high word of the increments from the chunk to the end of its run */
+DLK_DEV int4 make_rec(int bh, int slot, int next, uint64_t tot) {
+    return make_int4((bh & 0xffff) | (slot << 16), next, (int)(uint32_t)tot, (int)(uint32_t)(tot >> 32));
+}
+DLK_DEV int rec_bh(int x) { return (int)(short)(x & 0xffff); }
+DLK_DEV int rec_slot(int x) { return x >> 16; }
+DLK_DEV uint64_t rec_tot(int4 r) { return ((uint64_t)(uint32_t)r.w << 32) | (uint32_t)r.z; }
 
 constexpr int kDppWaveShr1 = 0x138;
 
@@ -373,6 +381,24 @@ DLK_DEV float wave_serial_sum(float c, float q) {
     for (int t = 1; t < 64; t++)
         y = u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(y), kDppWaveShr1, 0xf, 0xf, true)) + q0;
     return y;
+}
+
+/* c + q[0] + ... + q[63] in order, in every lane: each lane reads the whole
+ * chunk (an LDS broadcast) and adds it in registers; the running sum never
+ * leaves the lane, so the chain is 64 dependent adds with no lane exchange. */
+DLK_DEV float chunk_serial_sum(float c, const float *q) {
+    const float4 *src = (const float4 *)q;
+    float4 a[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) a[k] = src[k];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        c = c + a[k].x;
+        c = c + a[k].y;
+        c = c + a[k].z;
+        c = c + a[k].w;
+    }
+    return c;
 }
 
 /* Exact state of a walk between chunks: next chunk j, running value join_f(b, m). */
@@ -392,35 +418,45 @@ struct WalkOut {
 
 DLK_DEV int sreadi(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-/* Walks the running float sum c + q(0) + ... from state st over n elements:
- * runs are crossed with their integer totals, any other chunk is summed
- * element by element from its staged values (svals[smap[j] * 64 ...]).
- * Elements past n in the last chunk and in run totals must be zero. */
-__device__ __forceinline__ WalkOut walk_runs(int n, const int *smap, const float *svals, const Runs R, double thr_v,
+/* Smallest m on the grid of binade b with join_f(b, m) >= thr_v, saturated at 2^25. */
+DLK_DEV uint32_t grid_threshold(double thr_v, int b) {
+    const uint64_t t64 = ceil_div_pow2(thr_v, b - 23);
+    return t64 < (1ull << 25) ? (uint32_t)t64 : (1u << 25);
+}
+
+/* Walks the running float sum c + q(0) + ... from state st over n elements
+ * (one wave, uniform control flow): runs are crossed with their integer
+ * totals, any other chunk is summed element by element from its staged values
+ * (svals[slot * 64 ...], 16-byte aligned).  The record of the chunk after an
+ * element-level chunk is read while that chunk is summed.  Elements past n in
+ * the last chunk and in run totals must be zero. */
+__device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const float *svals, double thr_v,
                                              WalkState &st) {
     const int lane = lane_id();
     const int nch = (n + 63) >> 6;
-    const uint32_t top = 1u << 24;
-    int b = st.b, j = st.j;
-    uint32_t m = st.m;
-    uint64_t t64 = ceil_div_pow2(thr_v, b - 23);
-    uint32_t thr = t64 < (1ull << 25) ? (uint32_t)t64 : (1u << 25);
-    while (j < nch) {
-        if (sreadi(R.bh[j]) == b) {
-            const uint32_t lim = thr < top ? thr : top;
-            uint64_t tot = R.tot[j];
-            tot = ((uint64_t)(uint32_t)sreadi((int)(tot >> 32)) << 32) | (uint32_t)sreadi((int)(uint32_t)tot);
-            const int nx = sreadi(R.next[j]);
+    int b = sreadi(st.b), j = sreadi(st.j);
+    uint32_t m = (uint32_t)sreadi((int)st.m);
+    uint32_t thr = grid_threshold(thr_v, b);
+    if (j >= nch) return WalkOut{-1, join_f(b, m), -1};
+    int4 r = recs[j];
+    while (true) {
+        int x = sreadi(r.x);
+        if (rec_bh(x) == b) {
+            const uint32_t lim = thr < (1u << 24) ? thr : (1u << 24);
+            uint64_t tot = ((uint64_t)(uint32_t)sreadi(r.w) << 32) | (uint32_t)sreadi(r.z);
+            const int nx = sreadi(r.y);
             if ((uint64_t)m + tot < lim) {
                 m += (uint32_t)tot;
                 j = nx;
+                if (j >= nch) break;
+                r = recs[j];
                 continue;
             }
             /* the limit is reached inside the run: find the chunk */
             while (true) {
                 const int k = j + lane;
-                const uint64_t tk = k < nx ? R.tot[k] : 0;
-                const uint64_t tk1 = k + 1 < nx ? R.tot[k + 1] : 0;
+                const uint64_t tk = k < nx ? rec_tot(recs[k]) : 0;
+                const uint64_t tk1 = k + 1 < nx ? rec_tot(recs[k + 1]) : 0;
                 const int f = first_lane(ballot(k < nx && (uint64_t)m + (tot - tk1) >= lim));
                 if (f < 64) {
                     m += (uint32_t)(tot - readlane64(tk, f));
@@ -432,26 +468,35 @@ __device__ __forceinline__ WalkOut walk_runs(int n, const int *smap, const float
                 tot = tn;
                 j += 64;
             }
+            r = recs[j];
+            x = sreadi(r.x);
         }
-        const int sl = sreadi(smap[j]);
+        const int sl = rec_slot(x);
         if (sl < 0) {
             st.j = j;
             st.b = b;
             st.m = m;
             return WalkOut{-1, 0.0f, j};
         }
-        const int base = j * 64;
-        const int count = min(64, n - base);
-        const float qv = lane < count ? svals[sl * 64 + lane] : 0.0f;
-        const float y = wave_serial_sum(join_f(b, m), qv);
-        const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
-        if (f < count) return WalkOut{base + f, readlanef(y, f), -1};
+        const float *q = svals + sl * 64;
+        const int4 rn = recs[j + 1 < nch ? j + 1 : j];
+        const float c0 = join_f(b, m);
+        const float fin = chunk_serial_sum(c0, q);
+        if ((double)fin >= thr_v) {
+            /* the threshold is crossed in this chunk: find the element */
+            const int base = j * 64;
+            const int count = min(64, n - base);
+            const float y = wave_serial_sum(c0, lane < count ? q[lane] : 0.0f);
+            const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
+            return WalkOut{base + f, readlanef(y, f), -1};
+        }
         uint64_t m64;
-        split(readlanef(y, count - 1), b, m64);
-        m = (uint32_t)m64;
-        t64 = ceil_div_pow2(thr_v, b - 23);
-        thr = t64 < (1ull << 25) ? (uint32_t)t64 : (1u << 25);
-        j++;
+        split(fin, b, m64);
+        b = sreadi(b);
+        m = (uint32_t)sreadi((int)(uint32_t)m64);
+        thr = grid_threshold(thr_v, b);
+        if (++j >= nch) break;
+        r = rn;
     }
     st.j = j;
     st.b = b;

@@ -48,8 +48,7 @@ struct FullParams {
     uint32_t *sync;    /* [rows][kSyncWords] */
     uint64_t *pub;     /* [rows][G][kPubWords] */
     float *cvals;      /* [rows][G][kCandSlots][64] */
-    uint4 *wruns;      /* [rows][G][nch]: per chunk {binade, next chunk, run total lo, hi} */
-    int *wsmap;        /* [rows][G][nch]: staged slot of each chunk or -1 */
+    int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h) */
     float *wsvals;     /* [rows][G][stage_cap * 64]: staged chunks */
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;

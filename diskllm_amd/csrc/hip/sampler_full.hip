@@ -59,6 +59,34 @@ __device__ __forceinline__ void row_barrier(uint32_t *ctr, int G, uint32_t *stat
     __syncthreads();
 }
 
+/* Copies a slice's published walk data (records, staged values) into LDS; each
+ * thread issues its agent-scope loads before its LDS writes. */
+__device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64_t *wv, int nch, int nst, int4 *rec,
+                                                float *vals, int tt, int TT) {
+    for (int c0 = 0; c0 < nch; c0 += 2 * TT) {
+        const int ca = c0 + tt, cb = c0 + TT + tt;
+        uint64_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+        if (ca < nch) { a0 = at_ld64(&wr[2 * ca]); a1 = at_ld64(&wr[2 * ca + 1]); }
+        if (cb < nch) { b0 = at_ld64(&wr[2 * cb]); b1 = at_ld64(&wr[2 * cb + 1]); }
+        if (ca < nch) rec[ca] = make_int4((int)a0, (int)(a0 >> 32), (int)a1, (int)(a1 >> 32));
+        if (cb < nch) rec[cb] = make_int4((int)b0, (int)(b0 >> 32), (int)b1, (int)(b1 >> 32));
+    }
+    uint64_t *v2 = (uint64_t *)vals;
+    for (int i0 = 0; i0 < nst * 32; i0 += 4 * TT) {
+        uint64_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = i0 + k * TT + tt;
+            w[k] = i < nst * 32 ? at_ld64(&wv[i]) : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = i0 + k * TT + tt;
+            if (i < nst * 32) v2[i] = w[k];
+        }
+    }
+}
+
 /* Last workgroup of the row to leave returns the row's sync words to zero. */
 __device__ __forceinline__ void row_exit(uint32_t *sync, int G) {
     __builtin_amdgcn_s_waitcnt(0);
@@ -192,10 +220,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double *md = (double *)carve(q, 16 * 8);
     /* workgroup 0: walk data of later slices, prefetched while it walks its own */
     const int npf = g == 0 ? f.pf_slices : 0;
-    int *pf_bh = (int *)carve(q, (size_t)npf * nch * 4);
-    int *pf_next = (int *)carve(q, (size_t)npf * nch * 4);
-    uint64_t *pf_tot = (uint64_t *)carve(q, (size_t)npf * nch * 8);
-    int *pf_smap = (int *)carve(q, (size_t)npf * nch * 4);
+    int4 *pf_rec = (int4 *)carve(q, (size_t)npf * nch * 16);
     float *pf_vals = (float *)carve(q, (size_t)npf * f.pf_cap * 64 * 4);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
@@ -622,7 +647,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     __syncthreads();
     /* chunks the walk may have to open: mispredicted or near a binade edge,
-     * near the draw threshold, holding x, or holding a tie */
+     * near the draw threshold, holding x, or holding a tie; then the walk's
+     * record of every chunk (in the space of ce and cp, which are dead now) */
+    int4 *rec = (int4 *)ce;
     const double vthr = (double)u2f(f2u(r) + 1u);
     const double mu = 0x1p-8;
     for (int c = t; c < nch; c += T) {
@@ -637,6 +664,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             if (sl >= f.stage_cap - 1) sl = -1;         /* the last slot is the walk's spare */
         }
         smap[c] = sl;
+        rec[c] = make_rec(cbh[c], sl, rnext[c], rtot[c]);
     }
     __syncthreads();
 #pragma unroll
@@ -653,18 +681,16 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int64_t rg = (int64_t)row * G + g;
         /* agent-scope stores: the reader may sit on another XCD, whose L2 is not
          * coherent with this one for plain stores */
-        uint32_t *wr = (uint32_t *)(f.wruns + rg * nch);
-        uint32_t *wm = (uint32_t *)(f.wsmap + rg * nch);
-        uint32_t *wv = (uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
+        uint64_t *wr = (uint64_t *)(f.wrecs + rg * nch);
+        uint64_t *wv = (uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
         const int nst = min(misc[10], f.stage_cap - 1);
         for (int c = t; c < nch; c += T) {
-            at_st32(&wr[4 * c], (uint32_t)cbh[c]);
-            at_st32(&wr[4 * c + 1], (uint32_t)rnext[c]);
-            at_st32(&wr[4 * c + 2], (uint32_t)rtot[c]);
-            at_st32(&wr[4 * c + 3], (uint32_t)(rtot[c] >> 32));
-            at_st32(&wm[c], (uint32_t)smap[c]);
+            const int4 rc = rec[c];
+            at_st64(&wr[2 * c], (uint64_t)(uint32_t)rc.x | ((uint64_t)(uint32_t)rc.y << 32));
+            at_st64(&wr[2 * c + 1], (uint64_t)(uint32_t)rc.z | ((uint64_t)(uint32_t)rc.w << 32));
         }
-        for (int i = t; i < nst * 64; i += T) at_st32(&wv[i], f2u(svals[i]));
+        const uint64_t *sv2 = (const uint64_t *)svals;
+        for (int i = t; i < nst * 32; i += T) at_st64(&wv[i], sv2[i]);
         if (t == 0) at_st64(&mypub[kPubStaged], (uint64_t)nst);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -706,14 +732,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const bool own = gw == g;
         const int k = gw - 1;                      /* prefetch slot of a later slice */
         const bool pre = !own && k < npf && pf_ok[k];
-        int *w_bh = cbh, *w_next = rnext, *w_smap = smap;
-        uint64_t *w_tot = rtot;
-        float *w_vals = svals;
+        const int4 *w_rec = rec;
+        const float *w_vals = svals;
         if (pre) {
-            w_bh = pf_bh + k * nch;
-            w_next = pf_next + k * nch;
-            w_tot = pf_tot + k * nch;
-            w_smap = pf_smap + k * nch;
+            w_rec = pf_rec + k * nch;
             w_vals = pf_vals + (int64_t)k * f.pf_cap * 64;
         }
         if (!own && !pre) {
@@ -731,17 +753,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             __syncthreads();
             if (!misc[11]) break;
             const int64_t rg = (int64_t)row * G + gw;
-            const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
-            const int *wm = f.wsmap + rg * nch;
-            for (int c = t; c < nch; c += T) {
-                cbh[c] = (int)at_ld32(&wr[4 * c]);
-                rnext[c] = (int)at_ld32(&wr[4 * c + 1]);
-                rtot[c] = (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
-                smap[c] = (int)at_ld32((const uint32_t *)&wm[c]);
-            }
             const int nst = (int)at_ld64(&pubrow[gw * kPubWords + kPubStaged]);
-            const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
-            for (int i = t; i < nst * 64; i += T) svals[i] = u2f(at_ld32(&wv[i]));
+            fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch), (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64),
+                            nch, nst, rec, svals, t, T);
         }
         if (own && npf > 0 && t < 64)
             for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
@@ -757,17 +771,19 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         bool handed = false;
         for (int round = 0;; round++) {
             if (wave_id() == 0) {
-                const WalkOut o = walk_runs(n_loc, w_smap, w_vals, Runs{w_bh, w_tot, w_next}, vthr, st);
+                const WalkOut o = walk_recs(n_loc, w_rec, w_vals, vthr, st);
                 if (lane == 0) {
                     misc[13] = o.pos;
                     misc[14] = (int)f2u(o.value);
                     misc[15] = o.need;
                 }
             } else if (own && npf > 0 && round == 0) {
-                /* the other waves fetch the later slices' walk data meanwhile */
-                const int tt = t - 64, TT = T - 64;
-                for (int kk = 0; kk < npf; kk++) {
-                    const int gs = kk + 1;
+                /* the other waves fetch the later slices' walk data meanwhile:
+                 * one group of waves per slice, all slices at once */
+                const int nw = T / 64 - 1, gsz = max(1, nw / npf);
+                const int kk = (wave_id() - 1) / gsz;
+                if (kk < npf) {
+                    const int gs = kk + 1, tt = t - 64 - kk * gsz * 64, TT = gsz * 64;
                     bool ok = true;
                     if (lane == 0) {
                         uint32_t spins = 0;
@@ -775,23 +791,16 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                             if (++spins > kSpinLimit) { ok = false; break; }
                     }
                     ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
-                    if (!ok) break;                /* the walk will wait for it itself */
-                    const int nst = (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]);
-                    if (nst > f.pf_cap) continue;
-                    const int64_t rg = (int64_t)row * G + gs;
-                    const uint32_t *wr = (const uint32_t *)(f.wruns + rg * nch);
-                    const int *wm = f.wsmap + rg * nch;
-                    for (int c = tt; c < nch; c += TT) {
-                        pf_bh[kk * nch + c] = (int)at_ld32(&wr[4 * c]);
-                        pf_next[kk * nch + c] = (int)at_ld32(&wr[4 * c + 1]);
-                        pf_tot[kk * nch + c] =
-                            (uint64_t)at_ld32(&wr[4 * c + 2]) | ((uint64_t)at_ld32(&wr[4 * c + 3]) << 32);
-                        pf_smap[kk * nch + c] = (int)at_ld32((const uint32_t *)&wm[c]);
+                    const int nst = ok ? (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]) : 0;
+                    /* a slice that did not publish in time, or staged more than fits,
+                     * is fetched by the walk itself */
+                    if (ok && nst <= f.pf_cap) {
+                        const int64_t rg = (int64_t)row * G + gs;
+                        fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch),
+                                        (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64), nch, nst,
+                                        pf_rec + kk * nch, pf_vals + (int64_t)kk * f.pf_cap * 64, tt, TT);
+                        if (tt == 0) pf_ok[kk] = 1;
                     }
-                    const uint32_t *wv = (const uint32_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
-                    for (int i = tt; i < nst * 64; i += TT)
-                        pf_vals[(int64_t)kk * f.pf_cap * 64 + i] = u2f(at_ld32(&wv[i]));
-                    if (tt == 0) pf_ok[kk] = 1;
                 }
             }
             __syncthreads();
@@ -817,7 +826,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 svals[spare * 64 + t] = val;
             }
             __syncthreads();
-            if (t == 0) smap[need] = spare;
+            if (t == 0) {
+                smap[need] = spare;
+                rec[need].x = (rec[need].x & 0xffff) | (spare << 16);
+            }
             __syncthreads();
         }
         if (handed) break;
