@@ -145,7 +145,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     if (p.greedy || p.topk_on || p.minp_on) return 1;
     if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
-    if (vocab < 8192) return 1;
+    if (vocab < 8192 || (vocab & 3) != 0) return 1;   /* whole 16-byte groups per row */
     int G = (256 + rows - 1) / rows;
     if (G > kFullMaxG) G = kFullMaxG;
     if (G < 1) G = 1;

@@ -87,6 +87,27 @@ __device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64
     }
 }
 
+/* Issues the loads of a slice: 16-byte groups of logits (an out-of-range group
+ * reads the slice start instead) and, with a mask, each group's mask word. */
+template <int EPT, int J0, int J1>
+__device__ __forceinline__ void load_slice(const float *lg, const uint32_t *mk, int s0, int s1, int t, int T,
+                                           float4 *raw, uint32_t *mwd) {
+#pragma unroll
+    for (int j4 = J0; j4 < J1; j4++) {
+        const int i0 = s0 + 4 * (t + j4 * T);
+        raw[j4] = *(const float4 *)(lg + (i0 < s1 ? i0 : s0));
+        mwd[j4] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
+    }
+}
+
+
+constexpr int kClassNanPosInf = 1 | 2 | 512;       /* signalling NaN, quiet NaN, +inf */
+
+DLK_DEV float wave_max(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+
 /* Last workgroup of the row to leave returns the row's sync words to zero. */
 __device__ __forceinline__ void row_exit(uint32_t *sync, int G) {
     __builtin_amdgcn_s_waitcnt(0);
@@ -165,7 +186,7 @@ struct QSlice {
     const uint32_t *mk;
     const uint32_t *sbits;
     const uint32_t *spre;
-    const float *pval;
+    const float *pval;           /* penalised value of each patched id */
     int s0, x, topp;
     float M, inv_t, inv, inv3;
     const uint64_t *tab;
@@ -224,18 +245,36 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     float *pf_vals = (float *)carve(q, (size_t)npf * f.pf_cap * 64 * 4);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
-    const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
-    const float r = rand_f32_from(st);
-
-    /* ---- history first: each thread's id, and for an id inside this slice
-     *      its logit and mask word, gathered before the bulk loads so that
-     *      the penalties are computed while the slice is still in flight --- */
+    /* ---- history first: the ids, and for an id inside this slice its logit
+     *      and mask word, gathered before the bulk loads so that the penalties
+     *      are computed while the slice is still in flight ---------------------- */
     const int32_t *hist = nullptr;
     int nh = 0;
     if (p.hist_off) {
         hist = p.hist_ids + p.hist_off[row];
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
+    constexpr int kHistPer = 2;                    /* history ids per thread gathered early */
+    int hid[kHistPer];
+    float gx[kHistPer];
+    uint32_t gm[kHistPer];
+#pragma unroll
+    for (int k = 0; k < kHistPer; k++) hid[k] = t + k * T < nh ? hist[t + k * T] : -1;
+#pragma unroll
+    for (int k = 0; k < kHistPer; k++) {
+        gx[k] = 0.0f;
+        gm[k] = 0xffffffffu;
+        if (hid[k] >= s0 && hid[k] < s1) {
+            gx[k] = lg[hid[k]];
+            if (mk) gm[k] = mk[hid[k] >> 5];
+        }
+    }
+
+    /* ---- stream the slice into registers: every load issued before any use */
+    float4 raw[EPT / 4];
+    uint32_t mwd[EPT / 4];
+    load_slice<EPT, 0, EPT / 4>(lg, mk, s0, s1, t, T, raw, mwd);
+
     if (nh > p.plan.hcap) {
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
@@ -244,37 +283,24 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         row_exit(sync, G);
         return;
     }
-    int hid = -1;
-    float gx = 0.0f;
-    uint32_t gm = 0xffffffffu;
-    if (t < nh) {
-        hid = hist[t];
-        if (hid >= s0 && hid < s1) {
-            gx = lg[hid];
-            if (mk) gm = mk[hid >> 5];
-        }
-    }
-
-    /* ---- stream the slice into registers: every load issued before any use */
-    float4 raw[EPT / 4];
-    uint32_t mwd[EPT / 4];
-#pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        const int i0 = s0 + 4 * (t + j4 * T);
-        raw[j4] = *(const float4 *)(lg + (i0 + 3 < s1 ? i0 : s0));
-        mwd[j4] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
-    }
-
     /* ---- penalty patches of the ids inside this slice ------------------- */
     const int nw = S / 32;
     int *pfirst = L.pid;                           /* first history position of each patched id */
+    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
     for (int i = t; i < nw; i += T) sbits[i] = 0;
     for (int i = t; i < p.plan.hcap; i += T) { L.pcnt[i] = 0; pfirst[i] = 0x7fffffff; }
     if (t == 0) misc[5] = 0;
     __syncthreads();
-    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
     for (int i = t; i < nh; i += T) {
-        const int id = i == t ? hid : hist[i];
+        const int k = (i - t) / T;
+        int id = 0;
+        if (k < kHistPer) {
+#pragma unroll
+            for (int kk = 0; kk < kHistPer; kk++)
+                if (kk == k) id = hid[kk];
+        } else {
+            id = hist[i];
+        }
         hl[i] = id;
         if (id >= s0 && id < s1) atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
     }
@@ -305,15 +331,28 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         if (id < s0 || id >= s1) continue;
         const int slot = slice_rank(sbits, spre, id - s0);
         if (pfirst[slot] != i) continue;
+        const int k = (i - t) / T;
         float x;
         uint32_t m;
-        if (i == t) { x = gx; m = gm; }
-        else { x = lg[id]; m = mk ? mk[id >> 5] : 0xffffffffu; }
+        if (k < kHistPer) {
+            x = 0.0f;
+            m = 0u;
+#pragma unroll
+            for (int kk = 0; kk < kHistPer; kk++)
+                if (kk == k) { x = gx[kk]; m = gm[kk]; }
+        } else {
+            x = lg[id];
+            m = mk ? mk[id >> 5] : 0xffffffffu;
+        }
         if (!((m >> (id & 31)) & 1u)) x = -INFINITY;
         L.pval[slot] = penalize(x, L.pcnt[slot], p);
     }
+    const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
+    const float r = rand_f32_from(st);
     __syncthreads();
 
+    /* masked entries -inf, patched entries their penalised value; the row is a
+     * whole number of 4-element groups (the host routes other rows elsewhere) */
     float v[EPT];
     float tm = -INFINITY;
     bool bad = false;                              /* NaN or +inf after penalties */
@@ -321,33 +360,39 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int i0 = s0 + 4 * (t + j4 * T);
         float xs[4] = {raw[j4].x, raw[j4].y, raw[j4].z, raw[j4].w};
-        if (!(i0 + 3 < s1)) {
-            for (int c = 0; c < 4; c++) xs[c] = i0 + c < s1 ? lg[i0 + c] : -INFINITY;
+        if (i0 >= s1) xs[0] = xs[1] = xs[2] = xs[3] = -INFINITY;
+        if (mk) {
+            const uint32_t mw = mwd[j4] >> (i0 & 31);
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (!((mw >> c) & 1u)) xs[c] = -INFINITY;
         }
-        const uint32_t mw = mwd[j4] >> (i0 & 31);
         const int li0 = i0 - s0;
-        uint32_t pb = 0;
-        if (i0 < s1) pb = (sbits[li0 >> 5] >> (li0 & 31)) & 0xFu;
+        const uint32_t pb = i0 < s1 ? (sbits[li0 >> 5] >> (li0 & 31)) & 0xFu : 0u;
+        if (pb) {
+            /* patch slots of the group: consecutive ranks from the first marked entry */
+            int slot = slice_rank(sbits, spre, li0);
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if ((pb >> c) & 1u) xs[c] = L.pval[slot++];
+        }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int i = i0 + c;
-            float x = xs[c];
-            if (!((mw >> c) & 1u)) x = -INFINITY;
-            if ((pb >> c) & 1u) x = L.pval[slice_rank(sbits, spre, li0 + c)];
-            if (i >= s1) x = -INFINITY;
-            v[j4 * 4 + c] = x;
-            tm = fmaxf(tm, x);
-            bad |= !(x < INFINITY) && !(x == -INFINITY);
+            v[j4 * 4 + c] = xs[c];
+            tm = fmaxf(tm, xs[c]);
+            bad |= __builtin_amdgcn_class(xs[c], kClassNanPosInf);
         }
     }
     if (ballot(bad) != 0 && lane == 0) misc[5] = 1;
 
     /* ---- A: row maximum -------------------------------------------------- */
-    {
-        int dummy = 0;
-        block_argmax(tm, dummy, L);
+    tm = wave_max(tm);
+    if (lane == 0) ((float *)L.red)[wave_id()] = tm;
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < T / 64; w++) tm = fmaxf(tm, ((const float *)L.red)[w]);
+        at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
     }
-    if (t == 0) at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
     row_barrier(&sync[kSyncA], G, p.status);
     if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubMax]);
     __syncthreads();
@@ -421,7 +466,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         /* ---- p, its sums, and the chunks that may hold the top-p crossing ---- */
 #pragma unroll
         for (int j = 0; j < EPT; j++) v[j] = v[j] * inv;
-        if (g == 0) {
+        if (g == 0 && n_out > 0 && (p.out_cand_ids || p.out_cand_probs)) {
 #pragma unroll
             for (int j = 0; j < EPT; j++) {
                 const int i = 4 * (t + (j / 4) * T) + (j & 3);
@@ -581,11 +626,13 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int i = s0 + 4 * (t + (j / 4) * T) + (j & 3);
         v[j] = i <= x ? (topp ? v[j] * inv3 : v[j]) : 0.0f;
     }
-    if (g == 0) {
+    /* (a uniform test first: the log must not be evaluated speculatively when
+     * no log-probabilities are asked for) */
+    if (g == 0 && n_out > 0 && p.out_cand_logprobs) {
 #pragma unroll
         for (int j = 0; j < EPT; j++) {
             const int i = 4 * (t + (j / 4) * T) + (j & 3);
-            if (i < n_out && i < V && p.out_cand_logprobs)
+            if (i < n_out && i < V)
                 p.out_cand_logprobs[(int64_t)row * n_out + i] = v[j] > 0.0f ? (float)log((double)v[j]) : -INFINITY;
         }
     }
