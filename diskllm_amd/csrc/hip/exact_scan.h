@@ -45,6 +45,7 @@ namespace dlk {
 
 constexpr uint64_t kCap = 1ull << 62;       /* saturation: far above any binade */
 constexpr int kInvalidBinade = 0x7fff;
+constexpr int kEmptyRun = 0x7ffe;          /* walk_pairs: consecutive element chunks */
 
 struct Pair {
     uint64_t a0, a1;
@@ -401,6 +402,46 @@ DLK_DEV float chunk_serial_sum(float c, const float *q) {
     return c;
 }
 
+/* Staged values of one element-level chunk as chunk_split_sum reads them:
+ * lane 0 the first 32, every other lane the last 32; and the first half's sum. */
+struct HalfChunk {
+    float4 a[8];
+    double shalf;
+};
+DLK_DEV void load_half_chunk(const float *q, double shalf, HalfChunk &h) {
+    const float4 *src = (const float4 *)(q + (lane_id() == 0 ? 0 : 32));
+#pragma unroll
+    for (int k = 0; k < 8; k++) h.a[k] = src[k];
+    h.shalf = shalf;
+}
+
+/* c0 + q[0] + ... + q[63] in order, with half the dependent additions: lane 0
+ * adds q[0..32) to c0; lanes 1..63 each add q[32..64) to one of the 63
+ * consecutive floats around the predicted midpoint c0 + shalf.  32 float
+ * additions move the running value at most 16 of its ulps from the real sum,
+ * so the exact midpoint is among the starts -29 .. +33 floats from the
+ * prediction (the upward side allows for the ulp doubling at a binade edge);
+ * lane 0's result picks the lane that started there.  Should the midpoint
+ * ever fall outside, the second half is added in order from it (q in LDS). */
+DLK_DEV float chunk_split_sum(float c0, const HalfChunk &h, const float *q) {
+    const int lane = lane_id();
+    const uint32_t pu = f2u((float)((double)c0 + h.shalf));
+    float c = lane == 0 ? c0 : u2f(pu + (uint32_t)(lane - 30));
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        c = c + h.a[k].x;
+        c = c + h.a[k].y;
+        c = c + h.a[k].z;
+        c = c + h.a[k].w;
+    }
+    const uint32_t mid = (uint32_t)__builtin_amdgcn_readlane((int)f2u(c), 0);
+    const int d = (int)(mid - pu) + 30;
+    if (d >= 1 && d <= 63) return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(c), d));
+    float r = u2f(mid);
+    for (int k = 32; k < 64; k++) r = r + q[k];
+    return r;
+}
+
 /* Exact state of a walk between chunks: next chunk j, running value join_f(b, m). */
 struct WalkState {
     int j;
@@ -502,6 +543,120 @@ __device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const floa
     st.b = b;
     st.m = m;
     return WalkOut{-1, join_f(b, m), -1};
+}
+
+/* The common shape of a walk: run, element-level chunk, run, element-level
+ * chunk, ...  el[0..ne) lists the slice's element-level chunks in order with
+ * their staged slots (-1: not staged; the walk hands over to walk_recs before
+ * it).  Each lane holds one list entry and the run after it
+ * (binade and increments, when that run ends exactly at the next entry); each
+ * step crosses a run with two lane reads and sums the element chunk with
+ * chunk_split_sum, whose values were read during the previous step.
+ * Anything else (a run of another binade, the threshold inside a run, a chunk
+ * not in the list) continues in walk_recs from the exact state reached. */
+__device__ __forceinline__ WalkOut walk_pairs(int n, const int4 *recs, const float *svals, const double *shalf,
+                                              const int2 *el, int ne, double thr_v, WalkState &st) {
+    const int lane = lane_id();
+    const int nch = (n + 63) >> 6;
+    int b = sreadi(st.b), j = sreadi(st.j);
+    uint32_t m = (uint32_t)sreadi((int)st.m);
+    int bt;
+    uint64_t mt64;
+    split((float)thr_v, bt, mt64);
+    const uint32_t mt = (uint32_t)mt64;
+    const float thr_f = (float)thr_v;
+    for (int i0 = 0; i0 < ne; i0 += 64) {
+        const int cnt = min(64, ne - i0);
+        const int2 my_el = lane < cnt ? el[i0 + lane] : make_int2(nch, 0);
+        /* the run after entry `lane`, usable when it ends at the next entry */
+        int run_b = kInvalidBinade;
+        uint32_t run_t = 0;
+        {
+            const int nxt_chunk = __shfl_down(my_el.x, 1, 64);
+            const int c1 = my_el.x + 1;
+            if (lane + 1 < cnt && c1 < nxt_chunk) {
+                const int4 rr = recs[c1];
+                if (rr.y == nxt_chunk && rec_bh(rr.x) != kInvalidBinade) {
+                    run_b = rec_bh(rr.x);
+                    const uint64_t tt = rec_tot(rr);
+                    run_t = tt < (1ull << 25) ? (uint32_t)tt : (1u << 25);
+                }
+            } else if (lane + 1 < cnt && c1 == nxt_chunk) {
+                run_b = kEmptyRun;
+            }
+        }
+        int i = 0;
+        while (i < cnt && __builtin_amdgcn_readlane(my_el.x, i) < j) i++;
+        if (i == cnt) continue;
+        /* the run from j to the first entry */
+        {
+            const int e = __builtin_amdgcn_readlane(my_el.x, i);
+            if (e >= nch) break;
+            if (j < e) {
+                const int4 rr = recs[j];
+                const int rx = sreadi(rr.x), ry = sreadi(rr.y);
+                const uint64_t tot = ((uint64_t)(uint32_t)sreadi(rr.w) << 32) | (uint32_t)sreadi(rr.z);
+                const uint32_t lim = b == bt ? mt : (1u << 24);
+                if (b > bt || rec_bh(rx) != b || ry != e || (uint64_t)m + tot >= lim) goto general;
+                m += (uint32_t)tot;
+                j = e;
+            }
+        }
+        HalfChunk A, B;
+        {
+            const int sl = __builtin_amdgcn_readlane(my_el.y, i);
+            if (sl < 0) goto general;
+            load_half_chunk(svals + sl * 64, shalf[sl], A);
+        }
+        /* two steps per iteration, the values alternating between A and B */
+        while (true) {
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                HalfChunk &cur = half == 0 ? A : B;
+                HalfChunk &nxt = half == 0 ? B : A;
+                const int e = __builtin_amdgcn_readlane(my_el.x, i);
+                const int sl = __builtin_amdgcn_readlane(my_el.y, i);
+                const bool more = i + 1 < cnt && __builtin_amdgcn_readlane(my_el.x, i + 1) < nch &&
+                                  __builtin_amdgcn_readlane(my_el.y, i + 1) >= 0;
+                if (more) {
+                    const int sl2 = __builtin_amdgcn_readlane(my_el.y, i + 1);
+                    load_half_chunk(svals + sl2 * 64, shalf[sl2], nxt);
+                }
+                const float c0 = join_f(b, m);
+                const float c = chunk_split_sum(c0, cur, svals + sl * 64);
+                if (c >= thr_f) {
+                    /* the threshold is crossed in this chunk: find the element */
+                    const float *q = svals + sl * 64;
+                    const int base = e * 64, count = min(64, n - base);
+                    const float y = wave_serial_sum(c0, lane < count ? q[lane] : 0.0f);
+                    const int f = first_lane(ballot(lane < count && y >= thr_f));
+                    return WalkOut{base + f, readlanef(y, f), -1};
+                }
+                const uint32_t u = (uint32_t)sreadi((int)f2u(c)), ex = u >> 23;
+                if (ex <= 1) { b = -126; m = u; }
+                else { b = (int)ex - 127; m = (u & 0x7fffffu) | 0x800000u; }
+                j = e + 1;
+                __builtin_amdgcn_s_waitcnt(0xc07f);          /* lgkmcnt(0): the next values are in */
+                if (!more) goto next_batch;
+                /* the run to the next entry */
+                const int rb = __builtin_amdgcn_readlane(run_b, i);
+                i++;
+                if (rb != kEmptyRun) {
+                    const uint32_t rt = (uint32_t)__builtin_amdgcn_readlane((int)run_t, i - 1);
+                    const uint32_t lim = b == bt ? mt : (1u << 24);
+                    if (rb != b || b > bt || m + rt >= lim) goto general;
+                    m += rt;
+                    j = __builtin_amdgcn_readlane(my_el.x, i);
+                }
+            }
+        }
+    next_batch:;
+    }
+general:
+    st.j = j;
+    st.b = b;
+    st.m = m;
+    return walk_recs(n, recs, svals, thr_v, st);
 }
 
 }  // namespace dlk

@@ -36,6 +36,7 @@ enum : int {
     kPubCandPre = 6,   /* + s: double, slice-local exclusive p prefix at that chunk */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
     kPubStaged = 9,    /* staged chunks in the published walk data */
+    kPubNElem = 10,    /* entries of the published element-chunk list */
 };
 
 struct FullParams {
@@ -50,6 +51,8 @@ struct FullParams {
     float *cvals;      /* [rows][G][kCandSlots][64] */
     int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h) */
     float *wsvals;     /* [rows][G][stage_cap * 64]: staged chunks */
+    double *wshalf;    /* [rows][G][stage_cap]: first-half sum of each staged chunk */
+    int2 *wel;         /* [rows][G][stage_cap]: element-level chunks {chunk, slot} in order */
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;
     int force_exact;   /* test hook: send every row through the exact fallback */

@@ -59,10 +59,20 @@ __device__ __forceinline__ void row_barrier(uint32_t *ctr, int G, uint32_t *stat
     __syncthreads();
 }
 
-/* Copies a slice's published walk data (records, staged values) into LDS; each
- * thread issues its agent-scope loads before its LDS writes. */
-__device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64_t *wv, int nch, int nst, int4 *rec,
-                                                float *vals, int tt, int TT) {
+constexpr int kPfSkip = 0x100;                     /* prefetch: the group left the slice to the walk */
+
+/* Copies a slice's published walk data (records, staged values and their
+ * first-half sums, element-chunk list) into LDS; each thread issues its
+ * agent-scope loads before its LDS writes. */
+__device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64_t *wv, const uint64_t *wh,
+                                                const uint64_t *we, int nch, int nst, int ne, int4 *rec, float *vals,
+                                                double *half, int2 *el, int tt, int TT) {
+    for (int i0 = 0; i0 < max(nst, ne); i0 += TT) {
+        const int i = i0 + tt;
+        const uint64_t h = i < nst ? at_ld64(&wh[i]) : 0, e = i < ne ? at_ld64(&we[i]) : 0;
+        if (i < nst) half[i] = u2d(h);
+        if (i < ne) el[i] = make_int2((int)(uint32_t)e, (int)(uint32_t)(e >> 32));
+    }
     for (int c0 = 0; c0 < nch; c0 += 2 * TT) {
         const int ca = c0 + tt, cb = c0 + TT + tt;
         uint64_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
@@ -236,6 +246,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double *Pc = (double *)carve(q, (size_t)(nch + 1) * 8);      /* predicted running value */
     int *smap = (int *)carve(q, (size_t)nch * 4);
     float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
+    double *shalf = (double *)carve(q, (size_t)f.stage_cap * 8);  /* first-half sum of each staged chunk */
+    int2 *elist = (int2 *)carve(q, (size_t)f.stage_cap * 8);      /* element-level chunks {chunk, slot} */
     uint64_t *pc = (uint64_t *)carve(q, (size_t)G * kPubWords * 8);   /* published words, cached */
     int *misc = (int *)carve(q, 64 * 4);
     double *md = (double *)carve(q, 16 * 8);
@@ -243,6 +255,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const int npf = g == 0 ? f.pf_slices : 0;
     int4 *pf_rec = (int4 *)carve(q, (size_t)npf * nch * 16);
     float *pf_vals = (float *)carve(q, (size_t)npf * f.pf_cap * 64 * 4);
+    double *pf_shalf = (double *)carve(q, (size_t)npf * f.pf_cap * 8);
+    int2 *pf_el = (int2 *)carve(q, (size_t)npf * f.pf_cap * 8);
+    int *pf_ne = (int *)carve(q, (size_t)npf * 4);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
     /* ---- history first: the ids, and for an id inside this slice its logit
@@ -675,7 +690,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     if (t == 0) misc[10] = 0;
     __syncthreads();
-    /* runs: maximal stretches of valid chunks of one binade (nch <= T) */
+    /* runs: maximal stretches of valid chunks of one binade (nch <= T); and the
+     * position of each element-level chunk in the walk's list (the same scan,
+     * upper half-word) */
+    int elpos = -1;
     {
         const int c = t;
         const bool in = c < nch;
@@ -683,7 +701,11 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const bool vld = bc != kInvalidBinade;
         const bool end = in && (!vld || c == nch - 1 || cbh[c + 1] != bc);
         const uint64_t a = vld ? (uint64_t)ca[c] : 0;
-        const uint32_t run = block_excl_prefix_u32(end ? 1u : 0u, (uint32_t *)L.bi);
+        const bool isel = in && !vld;
+        const uint32_t both = block_excl_prefix_u32((end ? 1u : 0u) | (isel ? 0x10000u : 0u), (uint32_t *)L.bi);
+        const uint32_t run = both & 0xffffu;
+        if (isel) elpos = (int)(both >> 16);
+        if (t == T - 1) misc[17] = (int)(both >> 16) + (isel ? 1 : 0);
         const uint64_t ainc = block_incl_prefix_u64(a, (uint64_t *)L.red);
         if (end) { rend[run] = c; rpre[run] = ainc; }
         __syncthreads();
@@ -712,6 +734,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         smap[c] = sl;
         rec[c] = make_rec(cbh[c], sl, rnext[c], rtot[c]);
+        if (elpos >= 0 && elpos < f.stage_cap) elist[elpos] = make_int2(c, sl);
     }
     __syncthreads();
 #pragma unroll
@@ -720,8 +743,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int sl = smap[u >> 4];
         if (sl >= 0)
             for (int k = 0; k < 4; k++) svals[sl * 64 + (u & 15) * 4 + k] = v[4 * j4 + k];
+        if (ballot(sl >= 0) != 0) {
+            /* a chunk is one 16-lane row: the sum of its first 32 values */
+            double d = 0.0;
+            if ((u & 15) < 8)
+                d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
+            d = row_scan_d(d);
+            if (sl >= 0 && (lane & 15) == 15) shalf[sl] = d;
+        }
     }
     __syncthreads();
+    /* the walk's list of element-level chunks (a slot of -1: not staged) */
+    const int n_el = min(misc[17], f.stage_cap);
 
     /* ---- walk data of the later slices, published for workgroup 0 ------- */
     if (g > 0) {
@@ -738,6 +771,11 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         const uint64_t *sv2 = (const uint64_t *)svals;
         for (int i = t; i < nst * 32; i += T) at_st64(&wv[i], sv2[i]);
+        uint64_t *wh = (uint64_t *)(f.wshalf + rg * f.stage_cap);
+        uint64_t *we = (uint64_t *)(f.wel + rg * f.stage_cap);
+        for (int i = t; i < nst; i += T) at_st64(&wh[i], d2u(shalf[i]));
+        for (int i = t; i < n_el; i += T) at_st64(&we[i], (uint64_t)(uint32_t)elist[i].x | ((uint64_t)(uint32_t)elist[i].y << 32));
+        if (t == 0) at_st64(&mypub[kPubNElem], (uint64_t)n_el);
         if (t == 0) at_st64(&mypub[kPubStaged], (uint64_t)nst);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -773,20 +811,30 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         c_in = u2f((uint32_t)misc[12]);
     }
-    int *pf_ok = misc + 32;                        /* [pf_slices]: slice prefetched */
-    for (int gw = g;; gw++) {
-        const int s0w = gw * S, s1w = min(V, s0w + S);
+    /* prefetch state of later slice k+1: finished waves of its group, or
+     * kPfSkip when the group leaves it to the walk */
+    int *pf_ok = misc + 32;
+    const int pf_nw = T / 64 - 1, pf_gsz = npf > 0 ? max(1, pf_nw / npf) : 1;
+    if (npf > 0 && t < 64)
+        for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
+    for (int gw = g;;) {
         const bool own = gw == g;
         const int k = gw - 1;                      /* prefetch slot of a later slice */
-        const bool pre = !own && k < npf && pf_ok[k];
+        const bool pre = !own && k < npf && pf_ok[k] == pf_gsz;
         const int4 *w_rec = rec;
         const float *w_vals = svals;
+        const double *w_half = shalf;
+        const int2 *w_el = elist;
+        int cur_ne = own ? n_el : 0;
         if (pre) {
             w_rec = pf_rec + k * nch;
             w_vals = pf_vals + (int64_t)k * f.pf_cap * 64;
+            w_half = pf_shalf + (int64_t)k * f.pf_cap;
+            w_el = pf_el + (int64_t)k * f.pf_cap;
+            cur_ne = pf_ne[k];
         }
         if (!own && !pre) {
-            /* slice gw's runs and staged chunks into this workgroup's arrays */
+            /* slice gw's walk data into this workgroup's arrays */
             if (t == 0) {
                 uint32_t spins = 0, ok = 1;
                 while (!at_ld32(&sync[kSyncWalk + gw]))
@@ -801,13 +849,12 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             if (!misc[11]) break;
             const int64_t rg = (int64_t)row * G + gw;
             const int nst = (int)at_ld64(&pubrow[gw * kPubWords + kPubStaged]);
+            cur_ne = (int)at_ld64(&pubrow[gw * kPubWords + kPubNElem]);
             fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch), (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64),
-                            nch, nst, rec, svals, t, T);
+                            (const uint64_t *)(f.wshalf + rg * f.stage_cap), (const uint64_t *)(f.wel + rg * f.stage_cap),
+                            nch, nst, cur_ne, rec, svals, shalf, elist, t, T);
         }
-        if (own && npf > 0 && t < 64)
-            for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
         __syncthreads();
-        const int n_loc = min(s1w, x + 1) - s0w;
         WalkState st;
         {
             uint64_t m64;
@@ -818,19 +865,49 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         bool handed = false;
         for (int round = 0;; round++) {
             if (wave_id() == 0) {
-                const WalkOut o = walk_recs(n_loc, w_rec, w_vals, vthr, st);
+                const int n_loc = min(min(V, gw * S + S), x + 1) - gw * S;
+                WalkOut o = round == 0 ? walk_pairs(n_loc, w_rec, w_vals, w_half, w_el, cur_ne, vthr, st)
+                                       : walk_recs(n_loc, w_rec, w_vals, vthr, st);
+                /* workgroup 0 goes straight on through the prefetched slices */
+                int gc = gw;
+                float cin = c_in;
+                if (round == 0 && own && g == 0)
+                    while (o.pos < 0 && o.need < 0 && gc + 1 < G && gc < npf && x >= min(V, gc * S + S)) {
+                        uint32_t spins = 0;
+                        int pf;
+                        while ((pf = sreadi(__hip_atomic_load(&pf_ok[gc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))) <
+                                   pf_gsz && ++spins < kSpinLimit) {
+                        }
+                        if (pf != pf_gsz) break;
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                        cin = o.value;
+                        gc++;
+                        WalkState s2;
+                        {
+                            uint64_t m64;
+                            split(cin, s2.b, m64);
+                            s2.m = (uint32_t)m64;
+                            s2.j = 0;
+                        }
+                        const int kk = gc - 1;
+                        const int n2 = min(min(V, gc * S + S), x + 1) - gc * S;
+                        o = walk_pairs(n2, pf_rec + kk * nch, pf_vals + (int64_t)kk * f.pf_cap * 64,
+                                       pf_shalf + (int64_t)kk * f.pf_cap, pf_el + (int64_t)kk * f.pf_cap, pf_ne[kk], vthr,
+                                       s2);
+                    }
                 if (lane == 0) {
                     misc[13] = o.pos;
                     misc[14] = (int)f2u(o.value);
                     misc[15] = o.need;
+                    misc[18] = gc;
+                    misc[19] = (int)f2u(cin);
                 }
             } else if (own && npf > 0 && round == 0) {
                 /* the other waves fetch the later slices' walk data meanwhile:
                  * one group of waves per slice, all slices at once */
-                const int nw = T / 64 - 1, gsz = max(1, nw / npf);
-                const int kk = (wave_id() - 1) / gsz;
+                const int kk = (wave_id() - 1) / pf_gsz;
                 if (kk < npf) {
-                    const int gs = kk + 1, tt = t - 64 - kk * gsz * 64, TT = gsz * 64;
+                    const int gs = kk + 1, tt = t - 64 - kk * pf_gsz * 64, TT = pf_gsz * 64;
                     bool ok = true;
                     if (lane == 0) {
                         uint32_t spins = 0;
@@ -839,25 +916,35 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                     }
                     ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
                     const int nst = ok ? (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]) : 0;
+                    const int ne = ok ? (int)at_ld64(&pubrow[gs * kPubWords + kPubNElem]) : 0;
                     /* a slice that did not publish in time, or staged more than fits,
                      * is fetched by the walk itself */
-                    if (ok && nst <= f.pf_cap) {
+                    if (ok && nst <= f.pf_cap && ne <= f.pf_cap) {
                         const int64_t rg = (int64_t)row * G + gs;
                         fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch),
-                                        (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64), nch, nst,
-                                        pf_rec + kk * nch, pf_vals + (int64_t)kk * f.pf_cap * 64, tt, TT);
-                        if (tt == 0) pf_ok[kk] = 1;
+                                        (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64),
+                                        (const uint64_t *)(f.wshalf + rg * f.stage_cap),
+                                        (const uint64_t *)(f.wel + rg * f.stage_cap), nch, nst, ne, pf_rec + kk * nch,
+                                        pf_vals + (int64_t)kk * f.pf_cap * 64, pf_shalf + (int64_t)kk * f.pf_cap,
+                                        pf_el + (int64_t)kk * f.pf_cap, tt, TT);
+                        if (tt == 0) pf_ne[kk] = ne;
+                        /* this wave's part is in LDS before the count says so */
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                        if (lane == 0) atomicAdd(&pf_ok[kk], 1);
+                    } else if (lane == 0) {
+                        atomicOr(&pf_ok[kk], kPfSkip);
                     }
                 }
             }
             __syncthreads();
+            gw = misc[18];
             const int need = misc[15];
             if (need < 0) break;
-            if (!own) {
+            if (gw != g) {
                 /* a chunk of another slice that was not staged: hand the slice to
                  * its owner with its exact starting value */
                 if (t == 0) {
-                    at_st32(&sync[kSyncChainVal + gw], f2u(c_in));
+                    at_st32(&sync[kSyncChainVal + gw], (uint32_t)misc[19]);
                     __builtin_amdgcn_s_waitcnt(0);
                     at_st32(&sync[kSyncChain + gw], 1u);
                 }
@@ -867,7 +954,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             /* stage the chunk into the spare slot and resume the walk there */
             const int spare = f.stage_cap - 1;
             if (t < 64) {
-                QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, s0w, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
+                const int n_loc = min(min(V, gw * S + S), x + 1) - gw * S;
+                QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, gw * S, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
                 const int i = need * 64 + t;
                 const float val = i < n_loc ? qs(i) : 0.0f;
                 svals[spare * 64 + t] = val;
@@ -880,9 +968,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             __syncthreads();
         }
         if (handed) break;
+        const int s1w = min(V, gw * S + S);
         const int pos = misc[13];
         int token = -1;
-        if (pos >= 0) token = s0w + pos;
+        if (pos >= 0) token = gw * S + pos;
         else if (x < s1w) token = x;             /* nothing crossed r up to x: the last kept entry */
         if (token >= 0) {
             if (t == 0) {
@@ -902,6 +991,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             }
             break;
         }
+        gw++;
     }
     row_exit(sync, G);
 }
