@@ -720,7 +720,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      * record of every chunk (in the space of ce and cp, which are dead now) */
     int4 *rec = (int4 *)ce;
     const double vthr = (double)u2f(f2u(r) + 1u);
-    const double mu = 0x1p-8;
+    const double mu = 0x1p-9;
     for (int c = t; c < nch; c += T) {
         double a = Pc[c], b = Pc[c + 1];
         bool want = cbh[c] == kInvalidBinade ||
