@@ -49,7 +49,8 @@ struct FullParams {
     uint32_t *sync;    /* [rows][kSyncWords] */
     uint64_t *pub;     /* [rows][G][kPubWords] */
     float *cvals;      /* [rows][G][kCandSlots][64] */
-    int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h) */
+    int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h), stored as
+                          two arrays of 64-bit halves {x | y << 32}[nch] then {z | w << 32}[nch] */
     float *wsvals;     /* [rows][G][stage_cap * 64]: staged chunks */
     double *wshalf;    /* [rows][G][stage_cap]: first-half sum of each staged chunk */
     int2 *wel;         /* [rows][G][stage_cap]: element-level chunks {chunk, slot} in order */

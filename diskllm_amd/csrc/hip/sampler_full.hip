@@ -76,8 +76,8 @@ __device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64
     for (int c0 = 0; c0 < nch; c0 += 2 * TT) {
         const int ca = c0 + tt, cb = c0 + TT + tt;
         uint64_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-        if (ca < nch) { a0 = at_ld64(&wr[2 * ca]); a1 = at_ld64(&wr[2 * ca + 1]); }
-        if (cb < nch) { b0 = at_ld64(&wr[2 * cb]); b1 = at_ld64(&wr[2 * cb + 1]); }
+        if (ca < nch) { a0 = at_ld64(&wr[ca]); a1 = at_ld64(&wr[nch + ca]); }
+        if (cb < nch) { b0 = at_ld64(&wr[cb]); b1 = at_ld64(&wr[nch + cb]); }
         if (ca < nch) rec[ca] = make_int4((int)a0, (int)(a0 >> 32), (int)a1, (int)(a1 >> 32));
         if (cb < nch) rec[cb] = make_int4((int)b0, (int)(b0 >> 32), (int)b1, (int)(b1 >> 32));
     }
@@ -765,9 +765,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         uint64_t *wv = (uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
         const int nst = min(misc[10], f.stage_cap - 1);
         for (int c = t; c < nch; c += T) {
+            /* two arrays of halves, so that each store is contiguous across lanes */
             const int4 rc = rec[c];
-            at_st64(&wr[2 * c], (uint64_t)(uint32_t)rc.x | ((uint64_t)(uint32_t)rc.y << 32));
-            at_st64(&wr[2 * c + 1], (uint64_t)(uint32_t)rc.z | ((uint64_t)(uint32_t)rc.w << 32));
+            at_st64(&wr[c], (uint64_t)(uint32_t)rc.x | ((uint64_t)(uint32_t)rc.y << 32));
+            at_st64(&wr[nch + c], (uint64_t)(uint32_t)rc.z | ((uint64_t)(uint32_t)rc.w << 32));
         }
         const uint64_t *sv2 = (const uint64_t *)svals;
         for (int i = t; i < nst * 32; i += T) at_st64(&wv[i], sv2[i]);
