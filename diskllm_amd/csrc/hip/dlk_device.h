@@ -97,6 +97,44 @@ DLK_DEV double row_scan_d(double x) {
     x += dpp_row_d<kDppRowShr8>(x);
     return x;
 }
+/* 64-bit lane exchange by DPP: lanes the control leaves without a source (or
+ * rows outside row_mask) get `old`. */
+template <int CTRL, int ROWS = 0xf, bool BC = true>
+DLK_DEV uint64_t dpp_u64(uint64_t v, uint64_t old = 0) {
+    const int lo = __builtin_amdgcn_update_dpp((int)(uint32_t)old, (int)(uint32_t)v, CTRL, ROWS, 0xf, BC);
+    const int hi = __builtin_amdgcn_update_dpp((int)(uint32_t)(old >> 32), (int)(uint32_t)(v >> 32), CTRL, ROWS, 0xf, BC);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+/* Inclusive prefix over the 64 lanes by DPP (row shifts, then row broadcasts). */
+DLK_DEV double wave_incl_scan_d(double x) {
+    x += __longlong_as_double((long long)dpp_u64<kDppRowShr1>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp_u64<kDppRowShr2>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp_u64<kDppRowShr4>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp_u64<kDppRowShr8>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp_u64<kDppRowBcast15, 0xa, false>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp_u64<kDppRowBcast31, 0xc, false>((uint64_t)__double_as_longlong(x)));
+    return x;
+}
+DLK_DEV uint64_t wave_incl_scan_u64(uint64_t x) {
+    x += dpp_u64<kDppRowShr1>(x);
+    x += dpp_u64<kDppRowShr2>(x);
+    x += dpp_u64<kDppRowShr4>(x);
+    x += dpp_u64<kDppRowShr8>(x);
+    x += dpp_u64<kDppRowBcast15, 0xa, false>(x);
+    x += dpp_u64<kDppRowBcast31, 0xc, false>(x);
+    return x;
+}
+/* Maximum over the 64 lanes (every lane gets it). */
+DLK_DEV float wave_max_dpp(float v) {
+    const int ninf = (int)0xff800000u;
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowShr1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowShr2, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowShr4, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowShr8, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowBcast15, 0xa, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowBcast31, 0xc, 0xf, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 /* Inclusive wave prefix with saturation at `cap` (values <= cap). */
 DLK_DEV uint32_t wave_scan_sat_u32(uint32_t x, uint32_t cap) {
     uint32_t t;

@@ -113,10 +113,7 @@ __device__ __forceinline__ void load_slice(const float *lg, const uint32_t *mk, 
 
 constexpr int kClassNanPosInf = 1 | 2 | 512;       /* signalling NaN, quiet NaN, +inf */
 
-DLK_DEV float wave_max(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
-    return v;
-}
+DLK_DEV float wave_max(float v) { return wave_max_dpp(v); }
 
 /* Last workgroup of the row to leave returns the row's sync words to zero. */
 __device__ __forceinline__ void row_exit(uint32_t *sync, int G) {
@@ -136,16 +133,12 @@ __device__ __forceinline__ void block_excl_scan(double *P, int n, double *red) {
     const int b0 = t * per, b1 = min(n, b0 + per);
     double loc = 0.0;
     for (int c = b0; c < b1; c++) loc += P[c];
-    double inc = loc;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        double o = shfl_up(inc, d);
-        if (lane >= d) inc += o;
-    }
+    const double inc = wave_incl_scan_d(loc);
     if (lane == 63) red[w] = inc;
     __syncthreads();
-    double wbase = 0.0;
-    for (int k = 0; k < w; k++) wbase += red[k];
+    /* wave bases: a scan of the wave totals, one per lane */
+    const double wt = wave_incl_scan_d(lane < T / 64 ? red[lane] : 0.0);
+    const double wbase = w > 0 ? __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(wt), w - 1)) : 0.0;
     double run = wbase + inc - loc;
     __syncthreads();
     for (int c = b0; c < b1; c++) { double v = P[c]; P[c] = run; run += v; }
@@ -164,8 +157,8 @@ DLK_DEV uint32_t block_excl_prefix_u32(uint32_t v, uint32_t *red) {
     const uint32_t inc = wave_scan_sat_u32(v, 0xffffffffu);
     if (lane == 63) red[w] = inc;
     __syncthreads();
-    uint32_t base = 0;
-    for (int k = 0; k < w; k++) base += red[k];
+    const uint32_t wt = wave_scan_sat_u32(lane < (int)(blockDim.x / 64) ? red[lane] : 0u, 0xffffffffu);
+    const uint32_t base = w > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)wt, w - 1) : 0u;
     __syncthreads();
     return base + inc - v;
 }
@@ -173,16 +166,11 @@ DLK_DEV uint32_t block_excl_prefix_u32(uint32_t v, uint32_t *red) {
 /* Inclusive prefix of per-thread 64-bit values in thread order (red: 16 words). */
 DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     const int lane = lane_id(), w = wave_id();
-    uint64_t inc = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint64_t o = shfl_up(inc, d);
-        if (lane >= d) inc += o;
-    }
+    const uint64_t inc = wave_incl_scan_u64(v);
     if (lane == 63) red[w] = inc;
     __syncthreads();
-    uint64_t base = 0;
-    for (int k = 0; k < w; k++) base += red[k];
+    const uint64_t wt = wave_incl_scan_u64(lane < (int)(blockDim.x / 64) ? red[lane] : 0ull);
+    const uint64_t base = w > 0 ? readlane64(wt, w - 1) : 0ull;
     __syncthreads();
     return base + inc;
 }
@@ -404,9 +392,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     tm = wave_max(tm);
     if (lane == 0) ((float *)L.red)[wave_id()] = tm;
     __syncthreads();
-    if (t == 0) {
-        for (int w = 1; w < T / 64; w++) tm = fmaxf(tm, ((const float *)L.red)[w]);
-        at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
+    if (wave_id() == 0) {
+        tm = wave_max_dpp(lane < T / 64 ? ((const float *)L.red)[lane] : -INFINITY);
+        if (lane == 0) at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
     }
     row_barrier(&sync[kSyncA], G, p.status);
     if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubMax]);
@@ -570,12 +558,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                         const float *vals = f.cvals + ((int64_t)row * G + h) * kCandSlots * 64 + s * 64;
                         const int i = cg * 64 + lane;
                         double R = i < V ? (double)u2f(at_ld32((const uint32_t *)&vals[lane])) : 0.0;
-#pragma unroll
-                        for (int d = 1; d < 64; d <<= 1) {
-                            const double o = shfl_up(R, d);
-                            if (lane >= d) R += o;
-                        }
-                        R += R0;
+                        R = wave_incl_scan_d(R) + R0;
                         const double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
                         const int fl = first_lane(ballot(i < V && R * (1.0 + e) >= tau));
                         if (fl < 64) {
