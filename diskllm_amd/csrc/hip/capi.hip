@@ -187,22 +187,24 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     if (rows_per < 1) return 1;
     if (rows_per > rows) rows_per = rows;
     const size_t fb_bytes = r16(aggs_bytes(vocab));
-    const size_t n_pub = r16((size_t)rows_per * G * kPubWords * 8);
     const size_t n_cv = r16((size_t)rows_per * G * kCandSlots * 64 * 4);
     const size_t n_wr = r16((size_t)rows_per * G * nch * 16);
     const size_t n_wv = r16((size_t)rows_per * G * f.stage_cap * 64 * 4);
     const size_t n_wh = r16((size_t)rows_per * G * f.stage_cap * 8);      /* first-half sums; then the lists */
     WsView ws;
-    if (!workspace((size_t)rows_per * kSyncWords, n_pub + n_cv + n_wr + n_wv + 2 * n_wh + (size_t)rows_per * fb_bytes, ws))
+    /* the published words live in the zeroed counter region: they are zero
+     * between launches (the kernel returns them to zero) */
+    if (!workspace((size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
+                   n_cv + n_wr + n_wv + 2 * n_wh + (size_t)rows_per * fb_bytes, ws))
         return DLK_ERR_HIP;
     f.sync = ws.counters;
-    f.pub = (uint64_t *)ws.data;
-    f.cvals = (float *)(ws.data + n_pub);
-    f.wrecs = (int4 *)(ws.data + n_pub + n_cv);
-    f.wsvals = (float *)(ws.data + n_pub + n_cv + n_wr);
-    f.wshalf = (double *)(ws.data + n_pub + n_cv + n_wr + n_wv);
-    f.wel = (int2 *)(ws.data + n_pub + n_cv + n_wr + n_wv + n_wh);
-    f.fb = ws.data + n_pub + n_cv + n_wr + n_wv + 2 * n_wh;
+    f.pub = (uint64_t *)(ws.counters + (size_t)rows_per * kSyncWords);
+    f.cvals = (float *)ws.data;
+    f.wrecs = (int4 *)(ws.data + n_cv);
+    f.wsvals = (float *)(ws.data + n_cv + n_wr);
+    f.wshalf = (double *)(ws.data + n_cv + n_wr + n_wv);
+    f.wel = (int2 *)(ws.data + n_cv + n_wr + n_wv + n_wh);
+    f.fb = ws.data + n_cv + n_wr + n_wv + 2 * n_wh;
     f.fb_bytes = fb_bytes;
     for (int r0 = 0; r0 < rows; r0 += rows_per) {
         const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;

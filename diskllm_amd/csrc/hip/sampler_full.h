@@ -16,9 +16,6 @@ constexpr int kSyncWords = 64;       /* per-row synchronisation words */
 
 /* per-row sync words (all zero between launches) */
 enum : int {
-    kSyncA = 0,        /* row maximum published */
-    kSyncB = 1,        /* softmax partial sums published */
-    kSyncC = 2,        /* top-p partial sums + crossing chunks published */
     kSyncExit = 3,     /* workgroups finished */
     kSyncDone = 4,     /* token written */
     kSyncChain = 16,   /* + w: running value for workgroup w is ready */
@@ -47,7 +44,8 @@ struct FullParams {
     int pf_slices;     /* later slices whose walk data workgroup 0 prefetches into LDS */
     int pf_cap;        /* staged chunks of a prefetched slice that fit its buffer */
     uint32_t *sync;    /* [rows][kSyncWords] */
-    uint64_t *pub;     /* [rows][G][kPubWords] */
+    uint64_t *pub;     /* [rows][G][kPubWords], in the zeroed counter region: a word that readers
+                          poll carries kReady (bit 63) once written; all zero between launches */
     float *cvals;      /* [rows][G][kCandSlots][64] */
     int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h), stored as
                           two arrays of 64-bit halves {x | y << 32}[nch] then {z | w << 32}[nch] */

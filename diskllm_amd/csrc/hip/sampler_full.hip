@@ -42,22 +42,6 @@ DLK_DEV uint64_t at_ld64(const uint64_t *a) {
     return __hip_atomic_load((uint64_t *)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* All G workgroups of the row arrive; returns when all have (bounded wait). */
-__device__ __forceinline__ void row_barrier(uint32_t *ctr, int G, uint32_t *status) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t spins = 0;
-        while (at_ld32(ctr) < (uint32_t)G) {
-            if (++spins > kSpinLimit) {
-                if (status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-}
 
 constexpr int kPfSkip = 0x100;                     /* prefetch: the group left the slice to the walk */
 
@@ -115,14 +99,52 @@ constexpr int kClassNanPosInf = 1 | 2 | 512;       /* signalling NaN, quiet NaN,
 
 DLK_DEV float wave_max(float v) { return wave_max_dpp(v); }
 
-/* Last workgroup of the row to leave returns the row's sync words to zero. */
-__device__ __forceinline__ void row_exit(uint32_t *sync, int G) {
+/* Published words carry kReady (bit 63; every value stored in them leaves it
+ * clear) once written, so a reader polls the data itself instead of a separate
+ * arrival counter: one round trip less per barrier.  The row's words are zero
+ * between launches. */
+constexpr uint64_t kReady = 1ull << 63;
+
+/* Waits until word idx[k] (k < K) of every workgroup of the row carries kReady
+ * and copies it, flag cleared, into pc[h * kPubWords + idx[k]] for the whole
+ * workgroup.  Wave 0 polls, a word per lane; the wait is bounded. */
+template <int K>
+__device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const int (&idx)[K], uint64_t *pc,
+                                           uint32_t *status) {
+    if (wave_id() == 0) {
+        const int lane = lane_id(), n = G * K;
+        for (int b = 0; b < n; b += 64) {
+            const int q = b + lane;
+            const bool act = q < n;
+            const int off = act ? (q / K) * kPubWords + idx[q % K] : 0;
+            uint64_t w = 0;
+            uint32_t spins = 0;
+            while (true) {
+                if (act && !(w & kReady)) w = at_ld64(&pubrow[off]);
+                if (ballot(act && !(w & kReady)) == 0) break;
+                if (++spins > kSpinLimit) {
+                    if (lane == 0 && status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
+                    break;
+                }
+            }
+            if (act) pc[off] = w & ~kReady;
+        }
+    }
+    __syncthreads();
+}
+
+/* Last workgroup of the row to leave returns the row's sync and published words to zero. */
+__device__ __forceinline__ void row_exit(uint32_t *sync, uint64_t *pubrow, int G) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t old = __hip_atomic_fetch_add(&sync[kSyncExit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (uint32_t)(G - 1))
-            for (int i = 0; i < kSyncWords; i++) at_st32(&sync[i], 0u);
+    if (threadIdx.x < 64) {
+        uint32_t old = 0;
+        if (threadIdx.x == 0) old = __hip_atomic_fetch_add(&sync[kSyncExit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
+        if (old == (uint32_t)(G - 1)) {
+            for (int i = threadIdx.x; i < G * kPubWords; i += 64) at_st64(&pubrow[i], 0ull);
+            for (int i = threadIdx.x; i < kSyncWords; i += 64) at_st32(&sync[i], 0u);
+        }
     }
 }
 
@@ -283,7 +305,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             p.out_ids[row] = -1;
             if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
         }
-        row_exit(sync, G);
+        row_exit(sync, pubrow, G);
         return;
     }
     /* ---- penalty patches of the ids inside this slice ------------------- */
@@ -394,16 +416,17 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     __syncthreads();
     if (wave_id() == 0) {
         tm = wave_max_dpp(lane < T / 64 ? ((const float *)L.red)[lane] : -INFINITY);
-        if (lane == 0) at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32));
+        if (lane == 0) at_st64(&mypub[kPubMax], (uint64_t)f2u(tm) | ((uint64_t)(misc[5] != 0) << 32) | kReady);
     }
-    row_barrier(&sync[kSyncA], G, p.status);
-    if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubMax]);
-    __syncthreads();
+    {
+        const int idx[1] = {kPubMax};
+        row_gather(pubrow, G, idx, pc, p.status);
+    }
     float M = -INFINITY;
     bool row_bad = false;
     for (int h = 0; h < G; h++) {
-        M = fmaxf(M, u2f((uint32_t)pc[h]));
-        row_bad |= (pc[h] >> 32) != 0;
+        M = fmaxf(M, u2f((uint32_t)pc[h * kPubWords + kPubMax]));
+        row_bad |= (pc[h * kPubWords + kPubMax] >> 32) != 0;
     }
     if (g == 0 && t == 0) p.rng[row] = st;                  /* every workgroup has read it */
     const int n_out = p.n_out;
@@ -419,7 +442,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 if (p.out_cand_logprobs) p.out_cand_logprobs[o] = NAN;
             }
         }
-        row_exit(sync, G);
+        row_exit(sync, pubrow, G);
         return;
     }
 
@@ -442,15 +465,16 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     __syncthreads();
     block_excl_scan(ce, nch, L.red);                        /* ce[c]: e prefix at chunk c; ce[nch]: slice sum */
-    if (t == 0) at_st64(&mypub[kPubE], d2u(ce[nch]));
+    if (t == 0) at_st64(&mypub[kPubE], d2u(ce[nch]) | kReady);
 
     /* ---- B: softmax normaliser ------------------------------------------ */
-    row_barrier(&sync[kSyncB], G, p.status);
-    if (t < G) pc[t] = at_ld64(&pubrow[t * kPubWords + kPubE]);
-    __syncthreads();
+    {
+        const int idx[1] = {kPubE};
+        row_gather(pubrow, G, idx, pc, p.status);
+    }
     double Sapx = 0.0, EPw = 0.0;
     for (int h = 0; h < G; h++) {
-        double e = u2d(pc[h]);
+        double e = u2d(pc[h * kPubWords + kPubE]);
         if (h < g) EPw += e;
         Sapx += e;
     }
@@ -488,12 +512,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         __syncthreads();
         block_excl_scan(cp, nch, L.red);
-        if (t == 0) {
-            at_st64(&mypub[kPubP], d2u(cp[nch]));
-            if (g == 0) at_st64(&mypub[kPubP0], f2u(v[0]));
-            misc[1] = 0;
-        }
+        if (t == 0) misc[1] = 0;
         __syncthreads();
+        uint64_t cw[5] = {0, 0, 0, 0, 0};          /* NCand, CandChunk 0/1, CandPre 0/1 */
         const double tau = p.topp_thr;
         if (topp && p.top_p > 0.0f) {
             /* p-prefix predicted from the e-prefix: |p - e*inv| <= 2^-24 p each */
@@ -510,7 +531,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             __syncthreads();
             int ncand = misc[1];
             if (ncand > kCandSlots) {
-                if (t == 0) at_st64(&mypub[kPubNCand], 0xffffull);
+                cw[0] = 0xffffull;
             } else {
                 if (ncand == 2 && misc[2] > misc[3] && t == 0) { int tmp = misc[2]; misc[2] = misc[3]; misc[3] = tmp; }
                 __syncthreads();
@@ -523,18 +544,36 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                             for (int k = 0; k < 4; k++)
                                 at_st32((uint32_t *)&mycv[s * 64 + (u & 15) * 4 + k], f2u(v[4 * j4 + k]));
                     }
-                    if (t == 0) {
-                        at_st64(&mypub[kPubCandChunk + s], (uint64_t)(s0 / 64 + c));
-                        at_st64(&mypub[kPubCandPre + s], d2u(cp[c]));
-                    }
+                    cw[1 + s] = (uint64_t)(s0 / 64 + c);
+                    cw[3 + s] = d2u(cp[c]);
                 }
-                if (t == 0) at_st64(&mypub[kPubNCand], (uint64_t)ncand);
+                cw[0] = (uint64_t)ncand;
+            }
+        }
+        /* the candidate values are stored before the words that announce them */
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t == 0) {
+            at_st64(&mypub[kPubP], d2u(cp[nch]) | kReady);
+            at_st64(&mypub[kPubP0], (g == 0 ? (uint64_t)f2u(v[0]) : 0ull) | kReady);
+            at_st64(&mypub[kPubNCand], cw[0] | kReady);
+            for (int k2 = 0; k2 < 2; k2++) {
+                at_st64(&mypub[kPubCandChunk + k2], cw[1 + k2] | kReady);
+                at_st64(&mypub[kPubCandPre + k2], cw[3 + k2] | kReady);
             }
         }
 
         /* ---- C: top-p cut and its normaliser ------------------------------ */
-        row_barrier(&sync[kSyncC], G, p.status);
-        if (t < G * kPubWords) pc[t] = at_ld64(&pubrow[t]);
+        {
+            const int idx[7] = {kPubP, kPubP0, kPubNCand, kPubCandChunk, kPubCandChunk + 1, kPubCandPre,
+                                kPubCandPre + 1};
+            row_gather(pubrow, G, idx, pc, p.status);
+        }
+        /* every workgroup's candidate chunks (svals is free until the staging):
+         * slots that turn out unused are simply not looked at */
+        float *cvl = svals;
+        for (int i = t; i < G * kCandSlots * 64; i += T)
+            cvl[i] = u2f(at_ld32((const uint32_t *)(f.cvals + (int64_t)row * G * kCandSlots * 64 + i)));
         __syncthreads();
         if (wave_id() == 0) {
             /* one wave: each candidate chunk's running sum by a wave scan; any
@@ -555,9 +594,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                     for (int s = 0; s < (int)nc && okc && !found; s++) {
                         const int cg = (int)pc[h * kPubWords + kPubCandChunk + s];
                         const double R0 = RW + u2d(pc[h * kPubWords + kPubCandPre + s]);
-                        const float *vals = f.cvals + ((int64_t)row * G + h) * kCandSlots * 64 + s * 64;
+                        const float *vals = cvl + (h * kCandSlots + s) * 64;
                         const int i = cg * 64 + lane;
-                        double R = i < V ? (double)u2f(at_ld32((const uint32_t *)&vals[lane])) : 0.0;
+                        double R = i < V ? (double)vals[lane] : 0.0;
                         R = wave_incl_scan_d(R) + R0;
                         const double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
                         const int fl = first_lane(ballot(i < V && R * (1.0 + e) >= tau));
@@ -612,7 +651,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
             }
         }
-        row_exit(sync, G);
+        row_exit(sync, pubrow, G);
         return;
     }
 
@@ -790,7 +829,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         __syncthreads();
         if (misc[11] != 1) {
-            row_exit(sync, G);
+            row_exit(sync, pubrow, G);
             return;
         }
         c_in = u2f((uint32_t)misc[12]);
@@ -977,7 +1016,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         gw++;
     }
-    row_exit(sync, G);
+    row_exit(sync, pubrow, G);
 }
 
 }  // namespace dlk
