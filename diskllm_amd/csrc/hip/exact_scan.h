@@ -545,117 +545,162 @@ __device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const floa
     return WalkOut{-1, join_f(b, m), -1};
 }
 
+/* chunk_split_sum for the walk's inner loop: the candidate lane that started
+ * at the exact midpoint is read with one lane read at a scalar index, so the
+ * step has no branch.  mid: the exact running value after 32 elements; inw
+ * false when the midpoint fell outside the candidate window (the result is
+ * then not the chunk's end value). */
+DLK_DEV float split_step(float c, const HalfChunk &h, float &mid, bool &inw) {
+    const int lane = lane_id();
+    const uint32_t pu = (uint32_t)sreadi((int)f2u((float)((double)c + h.shalf)));
+    float y = lane == 0 ? c : u2f(pu + (uint32_t)(lane - 30));
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        y = y + h.a[k].x;
+        y = y + h.a[k].y;
+        y = y + h.a[k].z;
+        y = y + h.a[k].w;
+    }
+    mid = readlanef(y, 0);
+    const uint32_t d = f2u(mid) - pu + 30u;
+    inw = d - 1u < 63u;
+    return readlanef(y, inw ? (int)d : 0);
+}
+
 /* The common shape of a walk: run, element-level chunk, run, element-level
  * chunk, ...  el[0..ne) lists the slice's element-level chunks in order with
  * their staged slots (-1: not staged; the walk hands over to walk_recs before
- * it).  Each lane holds one list entry and the run after it
- * (binade and increments, when that run ends exactly at the next entry); each
- * step crosses a run with two lane reads and sums the element chunk with
- * chunk_split_sum, whose values were read during the previous step.
- * Anything else (a run of another binade, the threshold inside a run, a chunk
- * not in the list) continues in walk_recs from the exact state reached. */
+ * it).  Lane l holds list entry l and the run after it as one exact float
+ * step: R = its integer increments on the grid of its binade b, valid while the
+ * running value stays in [2^b, 2^(b+1)) (then every addition inside the run is
+ * exact on that grid, so the run adds exactly R).  A step sums the element
+ * chunk with split_step, whose values were read during the previous step, and
+ * crosses the run after it; the running value, the checks and the loop test
+ * stay in vector registers, one uniform branch per step.  Anything else (a run
+ * of another binade, the threshold inside a run or chunk, a chunk not in the
+ * list, the list's end) leaves the loop: the threshold inside the chunk is
+ * resolved here, the rest continues in walk_recs from the exact state reached. */
 __device__ __forceinline__ WalkOut walk_pairs(int n, const int4 *recs, const float *svals, const double *shalf,
                                               const int2 *el, int ne, double thr_v, WalkState &st) {
     const int lane = lane_id();
     const int nch = (n + 63) >> 6;
-    int b = sreadi(st.b), j = sreadi(st.j);
-    uint32_t m = (uint32_t)sreadi((int)st.m);
-    int bt;
-    uint64_t mt64;
-    split((float)thr_v, bt, mt64);
-    const uint32_t mt = (uint32_t)mt64;
     const float thr_f = (float)thr_v;
-    for (int i0 = 0; i0 < ne; i0 += 64) {
-        const int cnt = min(64, ne - i0);
-        const int2 my_el = lane < cnt ? el[i0 + lane] : make_int2(nch, 0);
-        /* the run after entry `lane`, usable when it ends at the next entry */
-        int run_b = kInvalidBinade;
-        uint32_t run_t = 0;
+    int j = sreadi(st.j);
+    float c = join_f(sreadi(st.b), (uint32_t)sreadi((int)st.m));
+    const int cnt = min(64, ne);
+    if (cnt <= 0) goto general;
+    {
+        const int2 my_el = lane < cnt ? el[lane] : make_int2(nch, -1);
+        /* the run after entry `lane`: fl 1 = it ends at the next entry, 2 = it
+         * ends at the slice's end; R, [lo, hi) as above (lo = +inf: unusable) */
+        float R = 0.0f, lo = INFINITY, hi = 0.0f;
+        int fl = 0;
         {
-            const int nxt_chunk = __shfl_down(my_el.x, 1, 64);
+            const int nx = __shfl_down(my_el.x, 1, 64), nsl = __shfl_down(my_el.y, 1, 64);
             const int c1 = my_el.x + 1;
-            if (lane + 1 < cnt && c1 < nxt_chunk) {
-                const int4 rr = recs[c1];
-                if (rr.y == nxt_chunk && rec_bh(rr.x) != kInvalidBinade) {
-                    run_b = rec_bh(rr.x);
+            const bool has_next = lane + 1 < cnt && nx < nch && nsl >= 0;
+            const int stop = has_next ? nx : nch;
+            if (my_el.x < nch && (has_next || lane + 1 == cnt)) {
+                if (c1 == stop) {
+                    lo = 0.0f;
+                    hi = INFINITY;
+                    fl = has_next ? 1 : 2;
+                } else if (c1 < stop) {
+                    const int4 rr = recs[c1];
+                    const int rb = rec_bh(rr.x);
                     const uint64_t tt = rec_tot(rr);
-                    run_t = tt < (1ull << 25) ? (uint32_t)tt : (1u << 25);
+                    if (rr.y == stop && rb != kInvalidBinade && rb > -126 && tt < (1ull << 24)) {
+                        R = ldexpf((float)tt, rb - 23);
+                        lo = ldexpf(1.0f, rb);
+                        hi = ldexpf(1.0f, rb + 1);
+                        fl = has_next ? 1 : 2;
+                    }
                 }
-            } else if (lane + 1 < cnt && c1 == nxt_chunk) {
-                run_b = kEmptyRun;
             }
         }
         int i = 0;
         while (i < cnt && __builtin_amdgcn_readlane(my_el.x, i) < j) i++;
-        if (i == cnt) continue;
-        /* the run from j to the first entry */
+        if (i == cnt) goto general;
         {
             const int e = __builtin_amdgcn_readlane(my_el.x, i);
-            if (e >= nch) break;
+            if (e >= nch) goto general;
             if (j < e) {
+                /* the run from j to the first entry */
                 const int4 rr = recs[j];
-                const int rx = sreadi(rr.x), ry = sreadi(rr.y);
-                const uint64_t tot = ((uint64_t)(uint32_t)sreadi(rr.w) << 32) | (uint32_t)sreadi(rr.z);
-                const uint32_t lim = b == bt ? mt : (1u << 24);
-                if (b > bt || rec_bh(rx) != b || ry != e || (uint64_t)m + tot >= lim) goto general;
-                m += (uint32_t)tot;
+                const int rb = rec_bh(sreadi(rr.x));
+                const uint64_t tt = ((uint64_t)(uint32_t)sreadi(rr.w) << 32) | (uint32_t)sreadi(rr.z);
+                if (sreadi(rr.y) != e || rb == kInvalidBinade || rb <= -126 || tt >= (1ull << 24)) goto general;
+                const float R0 = ldexpf((float)tt, rb - 23);
+                if (!(c >= ldexpf(1.0f, rb) && c + R0 < fminf(ldexpf(1.0f, rb + 1), thr_f))) goto general;
+                c = c + R0;
                 j = e;
             }
         }
-        HalfChunk A, B;
+        if (__builtin_amdgcn_readlane(my_el.y, i) < 0) goto general;
+        /* one buffer: the next chunk's values are read once this chunk's
+         * additions have consumed the registers, while the step finishes */
+        HalfChunk H;
         {
             const int sl = __builtin_amdgcn_readlane(my_el.y, i);
-            if (sl < 0) goto general;
-            load_half_chunk(svals + sl * 64, shalf[sl], A);
+            load_half_chunk(svals + sl * 64, shalf[sl], H);
+            /* nothing outstanding at the loop head, so the compiler's wait
+             * counting at the back edge starts from an empty count */
+            __builtin_amdgcn_s_waitcnt(0xc07f);
         }
-        /* two steps per iteration, the values alternating between A and B */
+        float ce, mid;
+        bool inw;
         while (true) {
 #pragma unroll
-            for (int half = 0; half < 2; half++) {
-                HalfChunk &cur = half == 0 ? A : B;
-                HalfChunk &nxt = half == 0 ? B : A;
-                const int e = __builtin_amdgcn_readlane(my_el.x, i);
-                const int sl = __builtin_amdgcn_readlane(my_el.y, i);
-                const bool more = i + 1 < cnt && __builtin_amdgcn_readlane(my_el.x, i + 1) < nch &&
-                                  __builtin_amdgcn_readlane(my_el.y, i + 1) >= 0;
-                if (more) {
-                    const int sl2 = __builtin_amdgcn_readlane(my_el.y, i + 1);
-                    load_half_chunk(svals + sl2 * 64, shalf[sl2], nxt);
+            for (int u = 0; u < 2; u++) {
+                const int fi = __builtin_amdgcn_readlane(fl, i);
+                ce = split_step(c, H, mid, inw);
+                {
+                    /* the next entry's values (this entry's again at the list's end) */
+                    const int sl2 = __builtin_amdgcn_readlane(my_el.y, fi == 1 ? i + 1 : i);
+                    load_half_chunk(svals + sl2 * 64, shalf[sl2], H);
                 }
-                const float c0 = join_f(b, m);
-                const float c = chunk_split_sum(c0, cur, svals + sl * 64);
-                if (c >= thr_f) {
-                    /* the threshold is crossed in this chunk: find the element */
-                    const float *q = svals + sl * 64;
-                    const int base = e * 64, count = min(64, n - base);
-                    const float y = wave_serial_sum(c0, lane < count ? q[lane] : 0.0f);
-                    const int f = first_lane(ballot(lane < count && y >= thr_f));
-                    return WalkOut{base + f, readlanef(y, f), -1};
+                const float Ri = readlanef(R, i), loi = readlanef(lo, i), hii = readlanef(hi, i);
+                const bool ok = inw && ce < thr_f && ce >= loi && ce + Ri < fminf(hii, thr_f);
+                if (!ok) goto leave;
+                c = ce + Ri;
+                if (fi != 1) {
+                    __builtin_amdgcn_s_waitcnt(0xc07f);
+                    return WalkOut{-1, c, -1};         /* the slice's end */
                 }
-                const uint32_t u = (uint32_t)sreadi((int)f2u(c)), ex = u >> 23;
-                if (ex <= 1) { b = -126; m = u; }
-                else { b = (int)ex - 127; m = (u & 0x7fffffu) | 0x800000u; }
-                j = e + 1;
-                __builtin_amdgcn_s_waitcnt(0xc07f);          /* lgkmcnt(0): the next values are in */
-                if (!more) goto next_batch;
-                /* the run to the next entry */
-                const int rb = __builtin_amdgcn_readlane(run_b, i);
                 i++;
-                if (rb != kEmptyRun) {
-                    const uint32_t rt = (uint32_t)__builtin_amdgcn_readlane((int)run_t, i - 1);
-                    const uint32_t lim = b == bt ? mt : (1u << 24);
-                    if (rb != b || b > bt || m + rt >= lim) goto general;
-                    m += rt;
-                    j = __builtin_amdgcn_readlane(my_el.x, i);
-                }
             }
         }
-    next_batch:;
+    leave:
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        {
+            /* entry i's chunk was summed from c; ce is its end value if inw */
+            const int e = __builtin_amdgcn_readlane(my_el.x, i);
+            const int sl = __builtin_amdgcn_readlane(my_el.y, i);
+            const float *q = svals + sl * 64;
+            if (!inw) {
+                float r = mid;
+                for (int k = 32; k < 64; k++) r = r + q[k];
+                ce = r;
+            }
+            if (ce >= thr_f) {
+                const int base = e * 64, count = min(64, n - base);
+                const float y = wave_serial_sum(c, lane < count ? q[lane] : 0.0f);
+                const int f = first_lane(ballot(lane < count && y >= thr_f));
+                return WalkOut{base + f, readlanef(y, f), -1};
+            }
+            c = ce;
+            j = e + 1;
+        }
     }
 general:
-    st.j = j;
-    st.b = b;
-    st.m = m;
+    {
+        int b;
+        uint64_t m64;
+        split(c, b, m64);
+        st.j = j;
+        st.b = sreadi(b);
+        st.m = (uint32_t)sreadi((int)(uint32_t)m64);
+    }
     return walk_recs(n, recs, svals, thr_v, st);
 }
 
