@@ -545,15 +545,16 @@ __device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const floa
     return WalkOut{-1, join_f(b, m), -1};
 }
 
-/* chunk_split_sum for the walk's inner loop: the candidate lane that started
- * at the exact midpoint is read with one lane read at a scalar index, so the
- * step has no branch.  mid: the exact running value after 32 elements; inw
- * false when the midpoint fell outside the candidate window (the result is
- * then not the chunk's end value). */
+/* chunk_split_sum for the walk's inner loop, without a branch: the candidate
+ * lane that started at the exact midpoint is read with a lane read at a scalar
+ * index (the candidates start from the prediction while it is still in vector
+ * registers; only the window offset goes through a scalar register).  mid:
+ * the exact running value after 32 elements; inw false when the midpoint fell
+ * outside the candidate window (the result is then not the chunk's end value). */
 DLK_DEV float split_step(float c, const HalfChunk &h, float &mid, bool &inw) {
     const int lane = lane_id();
-    const uint32_t pu = (uint32_t)sreadi((int)f2u((float)((double)c + h.shalf)));
-    float y = lane == 0 ? c : u2f(pu + (uint32_t)(lane - 30));
+    const uint32_t pv = f2u((float)((double)c + h.shalf));
+    float y = lane == 0 ? c : u2f(pv + (uint32_t)(lane - 30));
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         y = y + h.a[k].x;
@@ -561,6 +562,7 @@ DLK_DEV float split_step(float c, const HalfChunk &h, float &mid, bool &inw) {
         y = y + h.a[k].z;
         y = y + h.a[k].w;
     }
+    const uint32_t pu = (uint32_t)sreadi((int)pv);
     mid = readlanef(y, 0);
     const uint32_t d = f2u(mid) - pu + 30u;
     inw = d - 1u < 63u;
@@ -575,8 +577,10 @@ DLK_DEV float split_step(float c, const HalfChunk &h, float &mid, bool &inw) {
  * running value stays in [2^b, 2^(b+1)) (then every addition inside the run is
  * exact on that grid, so the run adds exactly R).  A step sums the element
  * chunk with split_step, whose values were read during the previous step, and
- * crosses the run after it; the running value, the checks and the loop test
- * stay in vector registers, one uniform branch per step.  Anything else (a run
+ * crosses the run after it.  Branches cost far more than arithmetic here (a
+ * uniform branch about 60 cycles against 5.5 for a dependent add), so the
+ * checks are combined without short-circuits and the loop test is the step's
+ * only branch; the state advances by selects.  Anything else (a run
  * of another binade, the threshold inside a run or chunk, a chunk not in the
  * list, the list's end) leaves the loop: the threshold inside the chunk is
  * resolved here, the rest continues in walk_recs from the exact state reached. */
@@ -648,30 +652,27 @@ __device__ __forceinline__ WalkOut walk_pairs(int n, const int4 *recs, const flo
             __builtin_amdgcn_s_waitcnt(0xc07f);
         }
         float ce, mid;
-        bool inw;
-        while (true) {
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int fi = __builtin_amdgcn_readlane(fl, i);
-                ce = split_step(c, H, mid, inw);
-                {
-                    /* the next entry's values (this entry's again at the list's end) */
-                    const int sl2 = __builtin_amdgcn_readlane(my_el.y, fi == 1 ? i + 1 : i);
-                    load_half_chunk(svals + sl2 * 64, shalf[sl2], H);
-                }
-                const float Ri = readlanef(R, i), loi = readlanef(lo, i), hii = readlanef(hi, i);
-                const bool ok = inw && ce < thr_f && ce >= loi && ce + Ri < fminf(hii, thr_f);
-                if (!ok) goto leave;
-                c = ce + Ri;
-                if (fi != 1) {
-                    __builtin_amdgcn_s_waitcnt(0xc07f);
-                    return WalkOut{-1, c, -1};         /* the slice's end */
-                }
-                i++;
+        bool inw, ok;
+        int fi;
+        /* one uniform branch per step: the loop test */
+        do {
+            fi = __builtin_amdgcn_readlane(fl, i);
+            ce = split_step(c, H, mid, inw);
+            {
+                /* the next entry's values (this entry's again at the list's end) */
+                const int sl2 = __builtin_amdgcn_readlane(my_el.y, fi == 1 ? i + 1 : i);
+                load_half_chunk(svals + sl2 * 64, shalf[sl2], H);
             }
-        }
-    leave:
+            const float Ri = readlanef(R, i), loi = readlanef(lo, i), hii = readlanef(hi, i);
+            const float cn = ce + Ri;
+            ok = inw & (ce < thr_f) & (ce >= loi) & (cn < fminf(hii, thr_f));
+            const bool go = ok & (fi == 1);
+            c = go ? cn : c;
+            i = go ? i + 1 : i;
+            if (!go) break;
+        } while (true);
         __builtin_amdgcn_s_waitcnt(0xc07f);
+        if (ok) return WalkOut{-1, ce + readlanef(R, i), -1};      /* the slice's end */
         {
             /* entry i's chunk was summed from c; ce is its end value if inw */
             const int e = __builtin_amdgcn_readlane(my_el.x, i);
