@@ -39,6 +39,8 @@
 #ifndef DLK_EXACT_SCAN_H
 #define DLK_EXACT_SCAN_H
 
+#include <type_traits>
+
 #include "dlk_device.h"
 
 namespace dlk {
@@ -369,37 +371,50 @@ DLK_DEV int rec_bh(int x) { return (int)(short)(x & 0xffff); }
 DLK_DEV int rec_slot(int x) { return x >> 16; }
 DLK_DEV uint64_t rec_tot(int4 r) { return ((uint64_t)(uint32_t)r.w << 32) | (uint32_t)r.z; }
 
-constexpr int kDppWaveShr1 = 0x138;
-
-/* Running float sum of the 64 lane values in lane order, exactly as a scalar
- * loop computes it: lane j ends with fl(...fl(fl(c + q_0) + q_1)... + q_j).
- * Each step shifts the partial sums one lane up (DPP wave_shr:1, lane 0 reads
- * 0) and adds the lane's own value; after step t lanes 0..t are final. */
-DLK_DEV float wave_serial_sum(float c, float q) {
-    const float q0 = lane_id() == 0 ? c + q : q;
-    float y = q0;
-#pragma unroll
-    for (int t = 1; t < 64; t++)
-        y = u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(y), kDppWaveShr1, 0xf, 0xf, true)) + q0;
-    return y;
+/* f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>) */
+template <int N, int I = 0, class F>
+DLK_DEV void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
 }
 
-/* c + q[0] + ... + q[63] in order, in every lane: each lane reads the whole
- * chunk (an LDS broadcast) and adds it in registers; the running sum never
- * leaves the lane, so the chain is 64 dependent adds with no lane exchange. */
-DLK_DEV float chunk_serial_sum(float c, const float *q) {
+/* r = lane == K ? y : cur: the one-lane mask is made in VCC by a scalar
+ * shift (no scalar register held, no lane compare), then one v_cndmask. */
+template <int K>
+DLK_DEV float select_lane(float cur, float y) {
+    float r;
+    asm("s_lshl_b64 vcc, 1, %3\n\tv_cndmask_b32_e32 %0, %1, %2, vcc" : "=v"(r) : "v"(cur), "v"(y), "n"(K) : "vcc");
+    return r;
+}
+
+/* c + q[0] + ... in order in every lane (the whole chunk read by every lane,
+ * an LDS broadcast), lane k keeping the running value after q[k]; returns the
+ * first of the first `count` positions whose value reaches thr_f (64 if none)
+ * and that value, and the chunk's end value in `fin`.  Values past count must
+ * be zero. */
+DLK_DEV int chunk_serial_find(float c, const float *q, float thr_f, int count, float &val, float &fin) {
     const float4 *src = (const float4 *)q;
     float4 a[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) a[k] = src[k];
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
+    float mine = 0.0f;
+    static_for<16>([&](auto kk) {
+        constexpr int k = decltype(kk)::value;
         c = c + a[k].x;
+        mine = select_lane<4 * k>(mine, c);
         c = c + a[k].y;
+        mine = select_lane<4 * k + 1>(mine, c);
         c = c + a[k].z;
+        mine = select_lane<4 * k + 2>(mine, c);
         c = c + a[k].w;
-    }
-    return c;
+        mine = select_lane<4 * k + 3>(mine, c);
+    });
+    fin = c;
+    const int f = first_lane(ballot(lane_id() < count && mine >= thr_f));
+    val = f < 64 ? readlanef(mine, f) : c;
+    return f;
 }
 
 /* Staged values of one element-level chunk as chunk_split_sum reads them:
@@ -522,15 +537,9 @@ __device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const floa
         const float *q = svals + sl * 64;
         const int4 rn = recs[j + 1 < nch ? j + 1 : j];
         const float c0 = join_f(b, m);
-        const float fin = chunk_serial_sum(c0, q);
-        if ((double)fin >= thr_v) {
-            /* the threshold is crossed in this chunk: find the element */
-            const int base = j * 64;
-            const int count = min(64, n - base);
-            const float y = wave_serial_sum(c0, lane < count ? q[lane] : 0.0f);
-            const int f = first_lane(ballot(lane < count && (double)y >= thr_v));
-            return WalkOut{base + f, readlanef(y, f), -1};
-        }
+        float fin, val;
+        const int f = chunk_serial_find(c0, q, (float)thr_v, min(64, n - j * 64), val, fin);
+        if (f < 64) return WalkOut{j * 64 + f, val, -1};   /* the threshold is crossed in this chunk */
         uint64_t m64;
         split(fin, b, m64);
         b = sreadi(b);
@@ -684,10 +693,9 @@ __device__ __forceinline__ WalkOut walk_pairs(int n, const int4 *recs, const flo
                 ce = r;
             }
             if (ce >= thr_f) {
-                const int base = e * 64, count = min(64, n - base);
-                const float y = wave_serial_sum(c, lane < count ? q[lane] : 0.0f);
-                const int f = first_lane(ballot(lane < count && y >= thr_f));
-                return WalkOut{base + f, readlanef(y, f), -1};
+                float fin, val;
+                const int f = chunk_serial_find(c, q, thr_f, min(64, n - e * 64), val, fin);
+                return WalkOut{e * 64 + f, val, -1};
             }
             c = ce;
             j = e + 1;
