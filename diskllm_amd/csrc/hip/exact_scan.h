@@ -508,7 +508,24 @@ __device__ __forceinline__ WalkOut walk_recs(int n, const int4 *recs, const floa
                 r = recs[j];
                 continue;
             }
-            /* the limit is reached inside the run: find the chunk */
+            /* the limit is reached inside the run: find the chunk, first the
+             * segment of ceil(len / 64) chunks that holds it (one ballot over
+             * the segment ends), then the chunk */
+            {
+                const int len = nx - j, step = (len + 63) >> 6;
+                if (step > 1) {
+                    const int nseg = (len + step - 1) / step;
+                    const int k1 = j + min((lane + 1) * step, len);
+                    const uint64_t t1 = lane < nseg && k1 < nx ? rec_tot(recs[k1]) : 0;
+                    const int sg = min(first_lane(ballot(lane < nseg && (uint64_t)m + (tot - t1) >= lim)), nseg - 1);
+                    if (sg > 0) {
+                        const uint64_t ts = readlane64(t1, sg - 1);     /* suffix total at the segment's start */
+                        m += (uint32_t)(tot - ts);
+                        tot = ts;
+                        j += sg * step;
+                    }
+                }
+            }
             while (true) {
                 const int k = j + lane;
                 const uint64_t tk = k < nx ? rec_tot(recs[k]) : 0;
