@@ -61,11 +61,13 @@ typedef struct {
     int *out_ids;
     pthread_barrier_t *bar;
     sampler *smp;
+    struct timespec *t0, *t1;    /* worker 0 only: after the start and end barriers */
 } refh_job;
 
 static void *refh_worker(void *arg) {
     refh_job *j = (refh_job *)arg;
     pthread_barrier_wait(j->bar);
+    if (j->t0) clock_gettime(CLOCK_MONOTONIC, j->t0);
     for (int r = j->r0; r < j->r1; r++) {
         float *l = j->work + (size_t)r * j->vocab;
         if (j->mask) {
@@ -85,10 +87,16 @@ static void *refh_worker(void *arg) {
         j->out_ids[r] = sampler_sample(j->smp, l, j->vocab);
     }
     pthread_barrier_wait(j->bar);
+    if (j->t1) clock_gettime(CLOCK_MONOTONIC, j->t1);
     return NULL;
 }
 
-/* Times `runs` passes over the batch; out_ms[run] = wall ms of one pass. */
+/* Times `runs` passes over the batch; out_ms[run] = wall ms of one pass, from
+ * the moment every worker has started to the moment the last one is done, read
+ * by worker 0 after each of two barriers among the workers only (a timing
+ * thread beside them would need a core of its own: on a host with exactly
+ * `threads` cores it can be scheduled late and read a start time after work
+ * has begun). */
 int refh_time_batch(const float *logits, int rows, int vocab, const int *hist_off,
                     const int *hist_ids, const uint32_t *mask, int mask_words, uint32_t order,
                     float rep, float freq, float pres, const sampler_config *cfg,
@@ -102,7 +110,8 @@ int refh_time_batch(const float *logits, int rows, int vocab, const int *hist_of
     pthread_barrier_t bar;
     for (int run = 0; run < runs; run++) {
         memcpy(work, logits, total * sizeof(float));
-        pthread_barrier_init(&bar, NULL, (unsigned)threads + 1);
+        pthread_barrier_init(&bar, NULL, (unsigned)threads);
+        struct timespec a, b;
         for (int t = 0; t < threads; t++) {
             refh_job *j = &jobs[t];
             j->work = work; j->vocab = vocab;
@@ -110,13 +119,10 @@ int refh_time_batch(const float *logits, int rows, int vocab, const int *hist_of
             j->hist_off = hist_off; j->hist_ids = hist_ids; j->mask = mask; j->mask_words = mask_words;
             j->order = order; j->rep = rep; j->freq = freq; j->pres = pres; j->cfg = *cfg;
             j->seeds = seeds; j->out_ids = out_ids; j->bar = &bar;
+            j->t0 = t == 0 ? &a : NULL;
+            j->t1 = t == 0 ? &b : NULL;
             pthread_create(&th[t], NULL, refh_worker, j);
         }
-        struct timespec a, b;
-        pthread_barrier_wait(&bar);
-        clock_gettime(CLOCK_MONOTONIC, &a);
-        pthread_barrier_wait(&bar);
-        clock_gettime(CLOCK_MONOTONIC, &b);
         for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
         pthread_barrier_destroy(&bar);
         out_ms[run] = (b.tv_sec - a.tv_sec) * 1e3 + (b.tv_nsec - a.tv_nsec) * 1e-6;
