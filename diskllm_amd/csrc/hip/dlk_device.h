@@ -82,6 +82,14 @@ DLK_DEV uint32_t row_scan_u32(uint32_t x) {
     x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowShr8, 0xf, 0xf, true);
     return x;
 }
+/* Inclusive prefix sum of floats within each 16-lane row. */
+DLK_DEV float row_scan_f(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowShr1, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowShr2, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowShr4, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowShr8, 0xf, 0xf, true));
+    return x;
+}
 template <int CTRL>
 DLK_DEV double dpp_row_d(double v) {
     uint64_t u = (uint64_t)__double_as_longlong(v);

@@ -168,6 +168,34 @@ __device__ __forceinline__ void block_excl_scan(double *P, int n, double *red) {
     __syncthreads();
 }
 
+/* e = expf((v - M) * inv_t) in place; returns the thread's e total in double
+ * and stores each
+ * chunk's e sum, rounded to float and summed in float, at ce[chunk]
+ * (relative error below 5 * 2^-24). */
+template <int EPT>
+__device__ __forceinline__ double exp_slice(float (&v)[EPT], float M, float inv_t, const uint64_t *tab, double *ce,
+                                            int t, int T) {
+    const int lane = lane_id();
+    double tsum = 0.0;
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        /* four at a time, each group summed at once: enough independent work
+         * to hide latency without widening live ranges into spills */
+        double d = 0.0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float e = dlk_expf_glibc_core(fmaxf((v[4 * j4 + k] - M) * inv_t, -200.0f), tab);
+            v[4 * j4 + k] = e;
+            d = k == 0 ? (double)e : d + (double)e;
+        }
+        tsum += d;
+        const float fs = row_scan_f((float)d);
+        if ((lane & 15) == 15) ce[(t + j4 * T) >> 4] = (double)fs;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return tsum;
+}
+
 /* Rank of marked bit li among the marked bits before it. */
 DLK_DEV int slice_rank(const uint32_t *bits, const uint32_t *pre, int li) {
     return (int)pre[li >> 5] + __popc(bits[li >> 5] & ((1u << (li & 31)) - 1u));
@@ -447,25 +475,19 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
 
     /* ---- e and its slice sums ------------------------------------------- */
+    /* e in place; the slice's e total in double (a bound-certified sum, any
+     * order), and float chunk sums, which only predict the top-p candidates */
     const float inv_t = p.inv_temp;
-#pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        /* four at a time, each group summed at once: enough independent work
-         * to hide latency without widening live ranges into spills */
-        double d = 0.0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float e = dlk_expf_glibc_core(fmaxf((v[4 * j4 + k] - M) * inv_t, -200.0f), L.tab);
-            v[4 * j4 + k] = e;
-            d = k == 0 ? (double)e : d + (double)e;
-        }
-        d = row_scan_d(d);
-        if ((lane & 15) == 15) ce[(t + j4 * T) >> 4] = d;
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    double tsum = exp_slice<EPT>(v, M, inv_t, L.tab, ce, t, T);
+    tsum = wave_incl_scan_d(tsum);
+    if (lane == 63) L.red[32 + wave_id()] = tsum;
     __syncthreads();
-    block_excl_scan(ce, nch, L.red);                        /* ce[c]: e prefix at chunk c; ce[nch]: slice sum */
-    if (t == 0) at_st64(&mypub[kPubE], d2u(ce[nch]) | kReady);
+    block_excl_scan(ce, nch, L.red);                        /* ce[c]: approximate e prefix at chunk c */
+    if (t == 0) {
+        double e_tot = 0.0;
+        for (int w2 = 0; w2 < T / 64; w2++) e_tot += L.red[32 + w2];
+        at_st64(&mypub[kPubE], d2u(e_tot) | kReady);
+    }
 
     /* ---- B: softmax normaliser ------------------------------------------ */
     {
@@ -517,8 +539,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         uint64_t cw[5] = {0, 0, 0, 0, 0};          /* NCand, CandChunk 0/1, CandPre 0/1 */
         const double tau = p.topp_thr;
         if (topp && p.top_p > 0.0f) {
-            /* p-prefix predicted from the e-prefix: |p - e*inv| <= 2^-24 p each */
-            const double dl = 0x1p-21;
+            /* p-prefix predicted from the e-prefix: |p - e*inv| <= 2^-24 p each,
+             * the float chunk sums within 5 * 2^-24, inv within 2^-24 */
+            const double dl = 0x1p-20;
             for (int c = t; c < nch; c += T) {
                 if (s0 + 64 * c >= s1) continue;
                 double lo = (double)inv * (EPw + ce[c]) * (1.0 - dl);
