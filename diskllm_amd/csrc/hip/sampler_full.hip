@@ -710,27 +710,28 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T;
         const int c = u >> 4;
-        int bh = predict_binade<24>(Pc[c]);
-        bool valid = bh == predict_binade<24>(Pc[c + 1]) && bh >= -100;
+        const int bh = predict_binade<24>(Pc[c]);
+        const bool valid = bh == predict_binade<24>(Pc[c + 1]) && bh >= -100;
         /* the increments are integers below 2^24 wherever the prediction holds,
          * so their float sum is exact; where it does not the sum still reaches
-         * 2^24 (non-negative terms, monotone rounding) and the walk opens the chunk */
+         * 2^24 (non-negative terms, monotone rounding) and the walk opens the
+         * chunk.  Computed for every lane (no branch: an invalid chunk's sum is
+         * not used); a tie saturates the lane's sum, so a chunk whose total
+         * reaches 2^24 -- a tie, or a sum that leaves the binade -- is opened. */
         float fsum = 0.0f;
         bool tie = false;
-        if (valid) {
-            for (int k = 0; k < 4; k++) {
-                const float xs = ldexpf(v[4 * j4 + k], 23 - bh);
-                const float n = rintf(xs);
-                tie |= fabsf(xs - n) == 0.5f;
-                fsum += n;
-            }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float xs = ldexpf(v[4 * j4 + k], 23 - bh);
+            const float n = rintf(xs);
+            tie |= fabsf(xs - n) == 0.5f;
+            fsum += n;
         }
-        uint32_t sum = (uint32_t)fminf(fsum, 0x1p25f);
+        uint32_t sum = tie ? (1u << 25) : (uint32_t)fminf(fsum, 0x1p25f);
         sum = row_scan_u32(sum);
-        tie = ((ballot(tie) >> (lane & 48)) & 0xffffull) != 0;
         if ((lane & 15) == 15) {
             ca[c] = sum;
-            cbh[c] = (valid && !tie) ? bh : kInvalidBinade;
+            cbh[c] = (valid && sum < (1u << 24)) ? bh : kInvalidBinade;
         }
     }
     if (t == 0) misc[10] = 0;
