@@ -79,6 +79,164 @@ def cpu_baseline(w, runs: int, threads_all: int) -> dict:
     return out
 
 
+# Algorithmic HBM bytes of the other workloads of the scope table, per step
+# (logits + per-row inputs + outputs; shared tables once per step).
+def other_bytes(w) -> int:
+    import numpy as np
+    V, rows = w.vocab, w.rows
+    W = (V + 31) // 32
+    if w.name == "C4":
+        csr = (V + 1) * 4 + int(w.dfa.data.size) + int(w.dfa.trans.size)
+        return csr + rows * (4 + W * 4)                 # CSR + table once, a state in and a mask row out per row
+    per = V * 4 + 8 + 4                                 # logits, rng state in/out, token id
+    if w.hist_off is not None:
+        per += int(np.max(np.diff(w.hist_off))) * 4     # history ids
+    if w.mask is not None or w.dfa is not None:
+        per += W * 4                                    # the row's mask words
+    per += w.n_out * 12                                 # candidate ids, probs, log-probs
+    return rows * per
+
+
+def run_other(name: str, args) -> int:
+    """One JSON line for workload C1, C3, C4 or C5 (parity-test configurations;
+    the headline line is C2): the step is one dlk_sample call (C4: one
+    dlk_dfa_mask call for its 16 rows), inputs resident in HBM, timed with HIP
+    events on the launch stream."""
+    import numpy as np
+    import torch
+    from diskllm_amd import api, workloads
+    from oracle import oracle as O
+    dev = torch.device("cuda:0")
+    w = workloads.CONFIGS[name]()
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    if name == "C4":
+        d = w.dfa
+        t_off = api._dev(np.asarray(d.offsets, np.uint32), dev)
+        t_dat = api._dev(np.asarray(d.data, np.uint8), dev)
+        t_st = api._dev(np.asarray(w.dfa_states, np.int32), dev)
+        t_tr = api._dev(np.ascontiguousarray(d.trans, np.uint8), dev)
+        W = (w.vocab + 31) // 32
+        out = torch.empty((w.rows, W), dtype=torch.int32, device=dev)
+        from diskllm_amd import _lib
+
+        def step():
+            rc = _lib.lib().dlk_dfa_mask(t_off.data_ptr(), t_dat.data_ptr(), w.vocab, t_tr.data_ptr(), d.trans.shape[0],
+                                         t_st.data_ptr(), w.rows, d.eos_id, d.accept & 0xFFFFFFFFFFFFFFFF,
+                                         out.data_ptr(), W, sh)
+            _lib.check(rc, "dlk_dfa_mask")
+        step()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint32)
+        n_ok = sum(int(np.array_equal(got[r], O.dfa_mask(d, int(w.dfa_states[r]), w.vocab))) for r in range(w.rows))
+        parity = f"{n_ok}/{w.rows} mask rows bit-identical to the oracle"
+    else:
+        db = api.to_device(w, device=dev)
+        params = api.params_of(w)
+
+        def step():
+            api.sample(db, params, sh)
+        step()
+        res = api.results(db)
+        check = list(range(min(w.rows, 32)))
+        orc = O.run_workload(w, check)
+        n_ok = int(np.sum(res["ids"][check] == orc["ids"]))
+        parity = f"{n_ok}/{len(check)} token ids bit-identical to the oracle (rows 0..{len(check) - 1})"
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    ms_dev = ev0.elapsed_time(ev1) / args.steps
+    nbytes = other_bytes(w)
+    achieved = nbytes / (ms_dev * 1e-3) / 1e9
+    line = {
+        "metric": f"{name}: rows/sec + achieved HBM GB/s (% of peak), batch {w.rows}, vocab {w.vocab}",
+        "value": round(w.rows / (ms_step * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8" if name == "C4" else "f32", "data": "synthetic",
+        "config": {"workload": f"{name}: " + " ".join(workloads.CONFIGS[name].__doc__.split()), "rows": w.rows,
+                   "vocab": w.vocab,
+                   "parallelism": "none (1 GPU)"},
+        "parity": parity,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                     "ms_per_launch": round(ms_dev, 5)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_other(w, args.cpu_runs)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_other(w, runs: int) -> dict:
+    """CPU time of the same step: C1/C3 the reference src/sampler.c (strict
+    build, masks applied as -inf first); C4 the oracle's byte-DFA walk (the DFA
+    mask has no counterpart in the reference); C5 both, on a 32-row sample."""
+    import numpy as np
+    from oracle import oracle as O
+    nthreads = min(16, os.cpu_count() or 1)
+    if w.name == "C4":
+        t0 = time.perf_counter()
+        for r in range(w.rows):
+            O.dfa_mask(w.dfa, int(w.dfa_states[r]), w.vocab)
+        dt = time.perf_counter() - t0
+        return {"value": round(w.rows / dt, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"all {w.rows} rows, oracle/oracle.c orc_dfa_mask, one pass"}
+    L = O.ref("strict")
+    if L is None:
+        return None
+    rows = list(range(min(w.rows, 32)))
+    lg = np.ascontiguousarray(w.logits[rows])
+    mask = None
+    mw = 0
+    dfa_s = 0.0
+    if w.mask is not None:
+        mask = np.ascontiguousarray(w.mask[rows])
+    elif w.dfa is not None:
+        t0 = time.perf_counter()
+        tab = {}
+        for r in rows:
+            st = int(w.dfa_states[r])
+            if st not in tab:
+                tab[st] = O.dfa_mask(w.dfa, st, w.vocab)
+        dfa_s = time.perf_counter() - t0
+        mask = np.ascontiguousarray(np.stack([tab[int(w.dfa_states[r])] for r in rows]))
+    if mask is not None:
+        mw = mask.shape[1]
+    hoff = hids = None
+    if w.hist_off is not None:
+        lists = [w.hist_ids[w.hist_off[r]:w.hist_off[r + 1]] for r in rows]
+        hoff = np.zeros(len(rows) + 1, np.int32)
+        hoff[1:] = np.cumsum([len(x) for x in lists])
+        hids = np.concatenate(lists).astype(np.int32)
+    cfg = O.SamplerConfig(w.temperature, w.top_k, w.top_p, w.min_p, 1)
+    th = min(nthreads, len(rows))
+    ms = np.zeros(runs, np.float64)
+    ids = np.zeros(len(rows), np.int32)
+    rc = L.refh_time_batch(lg, len(rows), w.vocab, hoff.ctypes.data if hoff is not None else None,
+                           hids.ctypes.data if hids is not None else None,
+                           mask.ctypes.data if mask is not None else None, mw, w.order, w.repeat_penalty,
+                           w.frequency_penalty, w.presence_penalty, C.byref(cfg),
+                           np.ascontiguousarray(w.seeds[rows]), th, runs, ms, ids)
+    if rc != 0:
+        return None
+    sec = float(np.median(ms)) / 1e3 + dfa_s
+    return {"value": round(len(rows) / sec, 1), "unit": "rows/s", "cores": th,
+            "kind": "reference",
+            "sample": f"rows 0..{len(rows) - 1}, median of {runs} runs, strict -std=c11 -O2 build"
+                      + ("; DFA mask rows by oracle/oracle.c orc_dfa_mask, one per distinct state" if w.dfa is not None else "")}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,6 +244,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
+                    help="C2 (default) is the headline line; the others are the scope table's parity "
+                         "configurations, measured the same way")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="instead of the benchmark, run --steps plain device-to-device copies of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -102,6 +263,8 @@ def main() -> int:
     from oracle import oracle as O
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.config != "C2":
+        return run_other(args.config, args)
     dev = torch.device("cuda:0")
     if args.copy_probe_mib:
         n = args.copy_probe_mib * (1 << 20) // 4
