@@ -108,12 +108,13 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     const int epts[5] = {64, 32, 16, 8, 4};
     for (int e : epts) {
         int g = (vocab + e * T - 1) / (e * T);
-        if ((int64_t)g * KP > 4096) break;
+        /* the merge keeps 4 words per slice (+2) in a T-word LDS array */
+        if ((int64_t)g * KP > 4096 || 4 * g + 2 > T) break;
         ept = e;
         G = g;
         if ((int64_t)rows * g >= 1024) break;
     }
-    if (G == 0 || 3 * G > T) return 1;
+    if (G == 0 || 4 * G + 2 > T) return 1;
     TopkParams f;
     memset(&f, 0, sizeof(f));
     f.p = p;

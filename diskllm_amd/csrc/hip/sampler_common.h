@@ -625,6 +625,64 @@ __device__ __forceinline__ int pipeline(const RowParams &p, const B &base, int n
     return d.pos >= 0 ? d.pos : last_kept;
 }
 
+/* pipeline for n <= 64 candidates, by one wave (lane j holds candidate j): the
+ * reference's sequential sums (src/sampler.c:177-233) run literally, in the
+ * same order, with every lane repeating them on values read lane by lane.  No
+ * block barrier; the caller broadcasts pos and S. */
+template <class B>
+__device__ __forceinline__ int pipeline_small(const RowParams &p, const B &base, int n, float r, Scal &S) {
+    const int lane = lane_id();
+    S.inv2 = 1.0f; S.inv3 = 1.0f; S.min_p = p.min_p;
+    S.minp_on = p.minp_on; S.minp_all = 0; S.topp_on = p.topp_on; S.cut = n - 1;
+    const float e = lane < n ? base.e(lane) : 0.0f;
+    /* softmax, :177-185 */
+    double sum = 0.0;
+    for (int j = 0; j < n; j++) sum += (double)readlanef(e, j);
+    S.inv = (float)(1.0 / sum);
+    const float pj = e * S.inv;
+    /* min-p, :188-202: survivors in order, all kept if none survives */
+    float t = pj;
+    if (S.minp_on) {
+        const uint64_t surv = ballot(lane < n && pj >= S.min_p);
+        S.minp_all = surv == 0;
+        S.cut = S.minp_all ? n - 1 : 63 - __builtin_clzll(surv);
+        const bool kept = lane < n && (S.minp_all || ((surv >> lane) & 1ull));
+        double s2 = 0.0;
+        for (int j = 0; j < n; j++)
+            if (S.minp_all || ((surv >> j) & 1ull)) s2 += (double)readlanef(pj, j);
+        S.inv2 = (float)(1.0 / s2);
+        t = kept ? pj * S.inv2 : 0.0f;
+    }
+    int last_kept = S.cut;
+    /* top-p, :205-222: the first position whose cumulative (float) reaches top_p */
+    if (S.topp_on) {
+        int x = last_kept;
+        double s3 = 0.0;
+        if (p.top_p <= 0.0f) {
+            x = S.minp_on && !S.minp_all ? __builtin_ctzll(ballot(lane < n && pj >= S.min_p)) : 0;
+            s3 = (double)readlanef(t, x);
+        } else {
+            double cumul = 0.0;
+            for (int j = 0; j <= last_kept; j++) {
+                cumul += (double)readlanef(t, j);
+                if ((float)cumul >= p.top_p) { x = j; break; }
+            }
+            s3 = cumul;
+        }
+        S.inv3 = (float)(1.0 / s3);
+        S.cut = x;
+        last_kept = x;
+        t = lane <= x ? t * S.inv3 : 0.0f;
+    }
+    /* draw, :225-233: the first position with r < cumul, else the last kept */
+    float cumul = 0.0f;
+    for (int j = 0; j <= last_kept; j++) {
+        cumul += readlanef(t, j);
+        if (r < cumul) return j;
+    }
+    return last_kept;
+}
+
 }  // namespace dlk
 
 #endif

@@ -291,20 +291,54 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     bool ok = !overflow && total <= f.buf_cap;
     int P = 64;
     if (ok) {
-        while (P < total) P <<= 1;
-        int at = 0;
-        for (int h = 0; h < G; h++) {
-            int kh = (int)sk[3 * h];
-            const uint64_t *ch = f.cands + ((int64_t)row * G + h) * f.KP;
-            for (int j = t; j < kh; j += T) {
-                uint64_t c = get64(&ch[j]);
-                float l = key_value((uint32_t)(c >> 32));
-                float s_ = (l - M) * R.inv_t;
-                buf[at + j] = ((uint64_t)desc_key(s_) << 32) | (c & 0xffffffffull);
-            }
-            at += kh;
+        /* every candidate read at once (one load per thread, not one round
+         * trip per slice): kept counts' prefix in LDS, then a binary search */
+        int *kpre = (int *)(sk + 3 * G);
+        uint32_t *tau = (uint32_t *)(kpre + G + 1);
+        if (t == 0) {
+            int a2 = 0;
+            for (int h = 0; h < G; h++) { kpre[h] = a2; a2 += (int)sk[3 * h]; }
+            kpre[G] = a2;
+            *tau = 0xffffffffu;
+            misc[46] = 0;
         }
-        for (int i = total + t; i < P; i += T) buf[i] = ~0ull;
+        __syncthreads();
+        /* a bound for the sort: list h is in logit order and s is monotone in
+         * the logit, so at least k entries have s >= the s of its k-th entry;
+         * anything whose s is below the best such bound is not in the top k */
+        for (int h = t; h < G; h += T) {
+            if ((int)sk[3 * h] >= k) {
+                const uint64_t c = get64(&f.cands[((int64_t)row * G + h) * f.KP + (k - 1)]);
+                atomicMin(tau, desc_key((key_value((uint32_t)(c >> 32)) - M) * R.inv_t));
+            }
+        }
+        __syncthreads();
+        const uint32_t tk = *tau;
+        for (int i0 = 0; i0 < total; i0 += T) {
+            const int i = i0 + t;
+            uint64_t e = 0;
+            bool take = false;
+            if (i < total) {
+                int lo = 0, hi = G;                  /* kpre[lo] <= i < kpre[hi] */
+                while (hi - lo > 1) {
+                    const int mid = (lo + hi) >> 1;
+                    if (kpre[mid] <= i) lo = mid; else hi = mid;
+                }
+                const uint64_t c = get64(&f.cands[((int64_t)row * G + lo) * f.KP + (i - kpre[lo])]);
+                const uint32_t key = desc_key((key_value((uint32_t)(c >> 32)) - M) * R.inv_t);
+                take = key <= tk;
+                e = ((uint64_t)key << 32) | (c & 0xffffffffull);
+            }
+            const uint64_t bal = ballot(take);
+            int base = 0;
+            if (lane == 0 && bal) base = atomicAdd(&misc[46], __popcll(bal));
+            base = shfl(base, 0);
+            if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = e;
+        }
+        __syncthreads();
+        const int nsort = misc[46];
+        while (P < nsort) P <<= 1;
+        for (int i = nsort + t; i < P; i += T) buf[i] = ~0ull;
         __syncthreads();
         bitonic_sort(buf, P);
         if (NF >= k) {
@@ -352,8 +386,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     CandBase cb{&R, buf};
     R.maxv = cb.s(0);
     Scal S;
-    unsigned char *reg = (unsigned char *)(buf + f.buf_cap);
-    int pos = pipeline(p, cb, k, r, reg, L, S);
+    int pos;
+    if (k <= 64) {
+        /* a few candidates: one wave runs the reference's loops literally */
+        if (w == 0) {
+            pos = pipeline_small(p, cb, k, r, S);
+            if (lane == 0) {
+                misc[40] = pos;
+                misc[41] = (int)f2u(S.inv); misc[42] = (int)f2u(S.inv2); misc[43] = (int)f2u(S.inv3);
+                misc[44] = S.minp_all; misc[45] = S.cut;
+            }
+        }
+        __syncthreads();
+        pos = misc[40];
+        S.inv = u2f((uint32_t)misc[41]); S.inv2 = u2f((uint32_t)misc[42]); S.inv3 = u2f((uint32_t)misc[43]);
+        S.min_p = p.min_p; S.minp_on = p.minp_on; S.minp_all = misc[44]; S.topp_on = p.topp_on; S.cut = misc[45];
+    } else {
+        unsigned char *reg = (unsigned char *)(buf + f.buf_cap);
+        pos = pipeline(p, cb, k, r, reg, L, S);
+    }
     if (t == 0) p.out_ids[row] = cb.token(pos);
     for (int j = t; j < n_out; j += T) {
         int64_t o = (int64_t)row * n_out + j;
