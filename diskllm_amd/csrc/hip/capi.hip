@@ -126,7 +126,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     while (bc < need || bc < p.plan.kp + 1024) bc <<= 1;
     f.buf_cap = bc;
     size_t lds = fixed_lds(p.plan) + r16((size_t)(f.S / 32) * 4) + r16((size_t)T * 4) + r16(64 * 4) +
-                 r16((size_t)bc * 8) + (p.greedy ? 0 : aggs_bytes(k));
+                 r16((size_t)bc * 8) + r16((size_t)kSelWords * 4) + (p.greedy ? 0 : aggs_bytes(k));
     if (lds > kMaxLds) return 1;
     size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
     size_t n_cand = (size_t)rows * G * KP * 8;

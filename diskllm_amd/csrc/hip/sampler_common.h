@@ -129,6 +129,49 @@ __device__ __forceinline__ void bitonic_sort(K *a, int n) {
     }
 }
 
+/* The key of rank r (0-based, ascending) among the n 32-bit keys key(i),
+ * i < n, 0 <= r < n: four rounds of 8-bit digits over an LDS histogram of 256
+ * counters (hist) and two broadcast words (bc); a handful of barriers where a
+ * bitonic sort of n keys takes log2(n)^2 / 2.  Every thread returns it. */
+template <class KF>
+__device__ __forceinline__ uint32_t block_select_u32(int n, int r, const KF &key, int *hist, int *bc) {
+    const int T = blockDim.x, t = threadIdx.x, lane = lane_id();
+    uint32_t prefix = 0;
+#pragma unroll 1
+    for (int round = 0; round < 4; round++) {
+        const int shift = 24 - 8 * round;
+        for (int i = t; i < 256; i += T) hist[i] = 0;
+        __syncthreads();
+        for (int i = t; i < n; i += T) {
+            const uint32_t k = key(i);
+            if (round == 0 || (k >> (shift + 8)) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (t < 64) {
+            const int c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+            const uint32_t sum4 = (uint32_t)(c0 + c1 + c2 + c3);
+            const uint32_t incl = wave_scan_sat_u32(sum4, 0xffffffffu);
+            const int excl = (int)(incl - sum4);
+            if (excl <= r && r < (int)incl) {
+                int rr = r - excl, d = 4 * lane;
+                if (rr >= c0) {
+                    rr -= c0; d++;
+                    if (rr >= c1) {
+                        rr -= c1; d++;
+                        if (rr >= c2) { rr -= c2; d++; }
+                    }
+                }
+                bc[0] = d;
+                bc[1] = rr;
+            }
+        }
+        __syncthreads();
+        prefix = (prefix << 8) | (uint32_t)bc[0];
+        r = bc[1];
+    }
+    return prefix;
+}
+
 /* Block reduce of (value, index): larger value wins, ties to the lower index;
  * NaN never wins (src/sampler.c:13 compares with '>'). */
 __device__ __forceinline__ void block_argmax(float &v, int &i, Lds &L) {

@@ -9,6 +9,8 @@
 namespace dlk {
 
 constexpr int kTopkThreads = 512;
+constexpr int kSelWords = 260;              /* radix-select histogram (256) + broadcast words */
+constexpr int kMergePerThread = 8;          /* merge: candidates per thread (G * KP <= 4096) */
 
 /* What each slice workgroup publishes (relaxed agent-scope atomic stores). */
 struct TopkSlot {

@@ -71,7 +71,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     uint32_t *sbits = (uint32_t *)carve(q, (size_t)(f.S / 32) * 4);          /* patched positions in slice */
     float *tmax = (float *)carve(q, (size_t)T * 4);
     int *misc = (int *)carve(q, 64 * 4);
-    uint64_t *buf = (uint64_t *)carve(q, (size_t)f.buf_cap * 8);           /* collect / merge / fallback */
+    int *selh = (int *)carve(q, kSelWords * 4);                           /* radix-select histogram */
+    uint64_t *buf = (uint64_t *)carve(q, (size_t)f.buf_cap * 8);           /* collect / merge / fallback (+ aggs) */
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
     const int32_t *hist = nullptr;
@@ -168,9 +169,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         /* ---- 4. threshold: the KP-th largest thread maximum ------------- */
         ((uint32_t *)tmax)[t] = asc_key(tm);
         __syncthreads();
-        bitonic_sort((uint32_t *)tmax, T);
         const int KP = f.KP;
-        uint32_t thr_key = ((uint32_t *)tmax)[T - min(KP, T)];   /* KP-th largest thread max */
+        const uint32_t *tk32 = (const uint32_t *)tmax;
+        const uint32_t thr_key = block_select_u32(T, T - min(KP, T), [&](int i) { return tk32[i]; }, selh, selh + 256);
         float thr = key_value(~thr_key);
         if (!(thr > -INFINITY)) thr = -INFINITY;
         /* ---- 5. collect finite elements >= thr ------------------------- */
@@ -336,7 +337,32 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
             if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = e;
         }
         __syncthreads();
-        const int nsort = misc[46];
+        int nsort = misc[46];
+        if (nsort > 64 && nsort >= k) {
+            /* only the k best are needed: the k-th smallest s-key by radix
+             * select, then the entries at or below it (k plus any ties) */
+            const uint32_t K = block_select_u32(nsort, k - 1, [&](int i) { return (uint32_t)(buf[i] >> 32); }, selh,
+                                                selh + 256);
+            uint64_t mine[kMergePerThread];
+#pragma unroll
+            for (int u = 0; u < kMergePerThread; u++) {
+                const int i = t + u * T;
+                mine[u] = i < nsort ? buf[i] : ~0ull;
+            }
+            if (t == 0) misc[47] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < kMergePerThread; u++) {
+                const bool take = (uint32_t)(mine[u] >> 32) <= K && mine[u] != ~0ull;
+                const uint64_t bal = ballot(take);
+                int base = 0;
+                if (lane == 0 && bal) base = atomicAdd(&misc[47], __popcll(bal));
+                base = shfl(base, 0);
+                if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = mine[u];
+            }
+            __syncthreads();
+            nsort = misc[47];
+        }
         while (P < nsort) P <<= 1;
         for (int i = nsort + t; i < P; i += T) buf[i] = ~0ull;
         __syncthreads();
