@@ -55,7 +55,7 @@ DLK_DEV float penalised(const RowParams &p, float x, int cnt) {
 }
 
 template <int EPT>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
+__global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
     const int g = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = lane_id(), w = wave_id();
@@ -74,6 +74,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     int *selh = (int *)carve(q, kSelWords * 4);                           /* radix-select histogram */
     uint64_t *buf = (uint64_t *)carve(q, (size_t)f.buf_cap * 8);           /* collect / merge / fallback (+ aggs) */
     if (t < 32) L.tab[t] = kExp2Tab[t];
+    const uint64_t rng0 = p.greedy ? 0ull : p.rng[row];     /* read early: only the merge uses (and writes) it */
 
     const int32_t *hist = nullptr;
     int nh = 0;
@@ -239,17 +240,37 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         buf[G + h] = ((uint64_t)get32(&s->nfin) << 32) | get32(&s->first_nan);
     }
     __syncthreads();
-    for (int h = 0; h < G; h++) {           /* identical in every thread, slice order */
-        float m = u2f((uint32_t)(buf[h] >> 32));
-        int a = (int)(uint32_t)buf[h];
-        if (m > M || (m == M && a < amax)) { M = m; amax = a; }
-        NF += (int)(buf[G + h] >> 32);
-        first_nan |= (int)((uint32_t)buf[G + h] & 1u);
-        irregular |= (int)((uint32_t)buf[G + h] & 2u);
-        total += (int)sk[3 * h];
-        overflow |= (int)sk[3 * h + 1] == -1;
+    if (w == 0) {
+        /* one wave: slices lane, lane + 64, ...; then lane reductions (the
+         * argmax keeps the larger value, ties to the lower index, as in order) */
+        for (int h = lane; h < G; h += 64) {
+            const float m = u2f((uint32_t)(buf[h] >> 32));
+            const int a = (int)(uint32_t)buf[h];
+            if (m > M || (m == M && a < amax)) { M = m; amax = a; }
+            NF += (int)(buf[G + h] >> 32);
+            first_nan |= (int)((uint32_t)buf[G + h] & 1u);
+            irregular |= (int)((uint32_t)buf[G + h] & 2u);
+            total += (int)sk[3 * h];
+            overflow |= (int)sk[3 * h + 1] == -1;
+        }
+        for (int m2 = 32; m2 >= 1; m2 >>= 1) {
+            const float om = shfl_xor(M, m2);
+            const int oa = shfl_xor(amax, m2);
+            if (om > M || (om == M && oa < amax)) { M = om; amax = oa; }
+            NF += shfl_xor(NF, m2);
+            first_nan |= shfl_xor(first_nan, m2);
+            irregular |= shfl_xor(irregular, m2);
+            total += shfl_xor(total, m2);
+            overflow |= shfl_xor(overflow, m2);
+        }
+        if (lane == 0) {
+            misc[48] = (int)f2u(M); misc[49] = amax; misc[50] = NF; misc[51] = first_nan;
+            misc[52] = irregular; misc[53] = total; misc[54] = overflow;
+        }
     }
     __syncthreads();
+    M = u2f((uint32_t)misc[48]); amax = misc[49]; NF = misc[50]; first_nan = misc[51];
+    irregular = misc[52]; total = misc[53]; overflow = misc[54];
     const int n_out = p.n_out;
     auto out_cands_empty = [&](float pr, float lpv, bool ids_idx, int kk) {
         for (int j = t; j < n_out; j += T) {
@@ -264,7 +285,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         out_cands_empty(0.0f, -INFINITY, false, 0);
         return;
     }
-    uint64_t st = xorshift64(p.rng[row]);
+    uint64_t st = xorshift64(rng0);
     const float r = rand_f32_from(st);
     __syncthreads();
     if (t == 0) p.rng[row] = st;
@@ -292,49 +313,43 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
     bool ok = !overflow && total <= f.buf_cap;
     int P = 64;
     if (ok) {
-        /* every candidate read at once (one load per thread, not one round
-         * trip per slice): kept counts' prefix in LDS, then a binary search */
-        int *kpre = (int *)(sk + 3 * G);
-        uint32_t *tau = (uint32_t *)(kpre + G + 1);
-        if (t == 0) {
-            int a2 = 0;
-            for (int h = 0; h < G; h++) { kpre[h] = a2; a2 += (int)sk[3 * h]; }
-            kpre[G] = a2;
-            *tau = 0xffffffffu;
-            misc[46] = 0;
-        }
+        /* every candidate read at once: thread t takes the slots t + u * T of
+         * the G x KP candidate array (slot j of slice h holds its (j+1)-th best
+         * logit when j < kept_h) */
+        uint32_t *tau = (uint32_t *)(sk + 3 * G);
+        if (t == 0) { *tau = 0xffffffffu; misc[46] = 0; }
         __syncthreads();
+        const int KP = f.KP, GK = G * KP;
+        const uint64_t *crow = f.cands + (int64_t)row * GK;
+        uint64_t cv[kMergePerThread];
+#pragma unroll
+        for (int u = 0; u < kMergePerThread; u++) {
+            const int i = t + u * T;
+            const int h = i / KP, j = i - h * KP;
+            cv[u] = (i < GK && j < (int)sk[3 * h]) ? get64(&crow[i]) : ~0ull;
+        }
         /* a bound for the sort: list h is in logit order and s is monotone in
          * the logit, so at least k entries have s >= the s of its k-th entry;
          * anything whose s is below the best such bound is not in the top k */
-        for (int h = t; h < G; h += T) {
-            if ((int)sk[3 * h] >= k) {
-                const uint64_t c = get64(&f.cands[((int64_t)row * G + h) * f.KP + (k - 1)]);
-                atomicMin(tau, desc_key((key_value((uint32_t)(c >> 32)) - M) * R.inv_t));
+#pragma unroll
+        for (int u = 0; u < kMergePerThread; u++) {
+            const int i = t + u * T;
+            if (cv[u] != ~0ull) {
+                cv[u] = ((uint64_t)desc_key((key_value((uint32_t)(cv[u] >> 32)) - M) * R.inv_t) << 32) |
+                        (cv[u] & 0xffffffffull);
+                if (i % KP == k - 1) atomicMin(tau, (uint32_t)(cv[u] >> 32));
             }
         }
         __syncthreads();
         const uint32_t tk = *tau;
-        for (int i0 = 0; i0 < total; i0 += T) {
-            const int i = i0 + t;
-            uint64_t e = 0;
-            bool take = false;
-            if (i < total) {
-                int lo = 0, hi = G;                  /* kpre[lo] <= i < kpre[hi] */
-                while (hi - lo > 1) {
-                    const int mid = (lo + hi) >> 1;
-                    if (kpre[mid] <= i) lo = mid; else hi = mid;
-                }
-                const uint64_t c = get64(&f.cands[((int64_t)row * G + lo) * f.KP + (i - kpre[lo])]);
-                const uint32_t key = desc_key((key_value((uint32_t)(c >> 32)) - M) * R.inv_t);
-                take = key <= tk;
-                e = ((uint64_t)key << 32) | (c & 0xffffffffull);
-            }
+#pragma unroll
+        for (int u = 0; u < kMergePerThread; u++) {
+            const bool take = cv[u] != ~0ull && (uint32_t)(cv[u] >> 32) <= tk;
             const uint64_t bal = ballot(take);
             int base = 0;
             if (lane == 0 && bal) base = atomicAdd(&misc[46], __popcll(bal));
             base = shfl(base, 0);
-            if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = e;
+            if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = cv[u];
         }
         __syncthreads();
         int nsort = misc[46];
@@ -370,12 +385,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams f) {
         if (NF >= k) {
             /* certify: every slice that kept only part of its finite elements
              * must have its last kept candidate strictly below the k-th s */
-            uint32_t kth = (uint32_t)(buf[k - 1] >> 32);
-            for (int h = 0; h < G; h++) {
+            const uint32_t kth = (uint32_t)(buf[k - 1] >> 32);
+            if (t == 0) misc[55] = 0;
+            __syncthreads();
+            for (int h = t; h < G; h += T) {
                 if ((int)sk[3 * h + 1] == 1) continue;
-                float l = key_value(sk[3 * h + 2]);
-                if (!(desc_key((l - M) * R.inv_t) > kth)) ok = false;
+                const float l = key_value(sk[3 * h + 2]);
+                if (!(desc_key((l - M) * R.inv_t) > kth)) misc[55] = 1;
             }
+            __syncthreads();
+            if (misc[55]) ok = false;
         } else {
             /* fewer finite entries than k: all of them plus the first k-NF
              * entries that are -inf, in index order */
