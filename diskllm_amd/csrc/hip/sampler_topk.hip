@@ -176,22 +176,27 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         float thr = key_value(~thr_key);
         if (!(thr > -INFINITY)) thr = -INFINITY;
         /* ---- 5. collect finite elements >= thr ------------------------- */
-        if (t == 0) misc[1] = 0;
+        /* a count per thread, one block prefix, then the writes */
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int j = 0; j < EPT; j++) cnt += (v[j] > -INFINITY && v[j] >= thr) ? 1u : 0u;
+        const uint32_t incl = wave_scan_sat_u32(cnt, 0xffffffffu);
+        if (lane == 63) misc[8 + w] = (int)incl;
         __syncthreads();
+        int at = (int)(incl - cnt), C = 0;
+        for (int u = 0; u < T / 64; u++) {
+            if (u < w) at += misc[8 + u];
+            C += misc[8 + u];
+        }
 #pragma unroll
         for (int j = 0; j < EPT; j++) {
-            const int i = s0 + 4 * (t + (j / 4) * T) + (j & 3);
-            float x = v[j];
-            bool take = x > -INFINITY && x >= thr;
-            uint64_t bal = ballot(take);
-            int base = 0;
-            if (lane == 0 && bal) base = atomicAdd(&misc[1], __popcll(bal));
-            base = shfl(base, 0);
-            int at = base + __popcll(bal & ((1ull << lane) - 1));
-            if (take && at < f.buf_cap) buf[at] = ((uint64_t)desc_key(x) << 32) | (uint32_t)i;
+            const float x = v[j];
+            if (x > -INFINITY && x >= thr) {
+                if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(x) << 32) | (uint32_t)(s0 + 4 * (t + (j / 4) * T) + (j & 3));
+                at++;
+            }
         }
         __syncthreads();
-        const int C = misc[1];
         if (C > f.buf_cap) {
             complete = -1;                     /* overflow: the merge falls back */
         } else {
