@@ -57,17 +57,18 @@ def profiled_traffic(kernel: str):
     return None
 
 
-def cpu_baseline(w, runs: int, threads_all: int) -> dict:
-    """The reference src/sampler.c (strict ISO C build in oracle/_ref) on the host:
+def cpu_baseline(w, runs: int, threads_all: int, kind: str = "strict") -> dict:
+    """The reference src/sampler.c (strict ISO C build in oracle/_ref, or with
+    kind "fast" the reference Makefile's -O3 -ffast-math build) on the host:
     penalties + sampler_sample for every row, rows split over pthreads."""
     import numpy as np
     from oracle import oracle as O
-    L = O.ref("strict")
+    L = O.ref(kind)
     if L is None:
         return None
     cfg = O.SamplerConfig(w.temperature, w.top_k, w.top_p, w.min_p, 1)
     out = {}
-    for th in sorted({1, threads_all}):
+    for th in (sorted({1, threads_all}) if kind == "strict" else [threads_all]):
         ms = np.zeros(runs, np.float64)
         ids = np.zeros(w.rows, np.int32)
         rc = L.refh_time_batch(np.ascontiguousarray(w.logits), w.rows, w.vocab, w.hist_off.ctypes.data,
@@ -340,6 +341,12 @@ def main() -> int:
                 "single_thread": round(cb[1]["value"], 1),
                 "ids_match_gpu": bool(np.array_equal(top["ids"], orc["ids"])),
             }
+            fast = cpu_baseline(w, args.cpu_runs, nthreads, "fast")
+            if fast is not None:
+                ff = fast[nthreads]
+                line["cpu_baseline"]["fast_math_build"] = {
+                    "value": round(ff["value"], 1), "cores": nthreads,
+                    "ids_agree_with_strict": f"{int(np.sum(ff['ids'] == top['ids']))}/{ROWS}"}
     print(json.dumps(line), flush=True)
     return 0
 
