@@ -68,7 +68,7 @@ class GrammarRow(C.Structure):
 EXPORTS = [
     # include/diskllm_amd.h
     "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
-    "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask",
+    "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
     # include/sampler.h
     "sampler_create", "sampler_free", "sampler_apply_repetition_penalty", "sampler_apply_presence_penalty",
     "sampler_sample", "greedy_sample",
@@ -117,6 +117,12 @@ def lib() -> C.CDLL:
         L.dlk_grammar_mask.restype = C.c_int
         L.dlk_grammar_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                        C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]
+        L.dlk_grammar_advance.restype = C.c_int
+        L.dlk_grammar_advance.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                          C.c_void_p]
+        L.dlk_sample_grammar.restype = C.c_int
+        L.dlk_sample_grammar.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p,
+                                         C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
         # include/sampler.h
         L.sampler_create.restype = C.c_void_p
         L.sampler_create.argtypes = [C.POINTER(SamplerConfig)]

@@ -59,6 +59,31 @@ __global__ __launch_bounds__(kMaskThreads) void grammar_mask_kernel(const uint32
     if (valid && lane == 0 && bal) atomicAdd(&valid[row], (int32_t)__popcll(bal));
 }
 
+/* diskllm_grammar_advance (src/core/grammar.c:248-256) as diskllm_sample_grammar
+ * calls it after the draw (src/core/sampler_api.c:65-70): unless the token is
+ * the EOS id, its string (up to its first NUL) is appended when buffer + string
+ * stays below 8191 bytes; here the row's validator and balance states take
+ * those bytes.  One thread per row. */
+__global__ void grammar_advance_kernel(const uint32_t *__restrict__ off, const uint8_t *__restrict__ bytes, int V,
+                                       dlk_grammar_row *states, const int32_t *__restrict__ tokens, int rows,
+                                       int eos_id) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int tok = tokens[row];
+    if (tok < 0 || tok >= V || tok == eos_id) return;
+    const uint32_t b0 = off[tok], b1 = off[tok + 1];
+    uint32_t len = 0;
+    while (b0 + len < b1 && bytes[b0 + len] != 0) len++;
+    dlk_grammar_row st = states[row];
+    if ((int64_t)st.bal.len + len >= DLK_GRAMMAR_BUF - 1) return;
+    for (uint32_t i = 0; i < len; i++) {
+        const uint8_t c = bytes[b0 + i];
+        dlk_scan_step(&st.scan, c);
+        dlk_balance_step(&st.bal, c);
+    }
+    states[row] = st;
+}
+
 }  // namespace dlk
 
 extern "C" int dlk_grammar_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const dlk_grammar_row *states,
@@ -72,4 +97,26 @@ extern "C" int dlk_grammar_mask(const uint32_t *off, const uint8_t *bytes, int v
                        dim3(kMaskThreads), 0, stream, off, bytes, vocab, states, eos_id, mask, mask_ld, logits, ld,
                        valid);
     return hipGetLastError() == hipSuccess ? DLK_OK : DLK_ERR_HIP;
+}
+
+extern "C" int dlk_grammar_advance(const uint32_t *off, const uint8_t *bytes, int vocab, dlk_grammar_row *states,
+                                   const int32_t *tokens, int rows, int eos_id, hipStream_t stream) {
+    using namespace dlk;
+    if (!off || !bytes || !states || !tokens || vocab <= 0 || rows <= 0) return DLK_ERR_INVALID;
+    hipLaunchKernelGGL(grammar_advance_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, off, bytes, vocab, states,
+                       tokens, rows, eos_id);
+    return hipGetLastError() == hipSuccess ? DLK_OK : DLK_ERR_HIP;
+}
+
+extern "C" int dlk_sample_grammar(const dlk_batch *b, int rows, int vocab, const dlk_sample_params *params,
+                                  const uint32_t *off, const uint8_t *bytes, dlk_grammar_row *states, int eos_id,
+                                  hipStream_t stream) {
+    if (!b || !params || !b->mask || b->mask_row) return DLK_ERR_INVALID;
+    /* the batch's mask buffer is written here, then read by the draw */
+    int rc = dlk_grammar_mask(off, bytes, vocab, states, rows, eos_id, (uint32_t *)b->mask, b->mask_ld, nullptr, 0,
+                              nullptr, stream);
+    if (rc != DLK_OK) return rc;
+    rc = dlk_sample(b, rows, vocab, params, stream);
+    if (rc != DLK_OK) return rc;
+    return dlk_grammar_advance(off, bytes, vocab, states, b->out_ids, rows, eos_id, stream);
 }

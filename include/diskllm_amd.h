@@ -166,6 +166,25 @@ int dlk_grammar_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const
                      int rows, int eos_id, uint32_t *mask, int64_t mask_ld, float *logits, int64_t ld,
                      int32_t *valid, hipStream_t stream);
 
+/* The device form of diskllm_grammar_advance (src/core/grammar.c:248-256) as
+ * diskllm_sample_grammar applies it after the draw (src/core/sampler_api.c:
+ * 65-70): for each row whose token (device array) is not eos_id, that token's
+ * string (up to its first NUL) is appended to the row's buffer when buffer +
+ * string stays below 8191 bytes, i.e. the row's states take those bytes. */
+int dlk_grammar_advance(const uint32_t *off, const uint8_t *bytes, int vocab, dlk_grammar_row *states,
+                        const int32_t *tokens, int rows, int eos_id, hipStream_t stream);
+
+/* One constrained decoding step for a batch, on the device, replacing
+ * diskllm_sample_grammar (src/core/sampler_api.c:48-73) per row: the grammar
+ * mask of each row's state (written to batch->mask, which must be a
+ * [rows, mask_ld] buffer, and mask_row NULL), penalties and the draw as
+ * dlk_sample (params->order DLK_ORDER_REFERENCE gives the reference's order),
+ * then the rows' states advanced by the drawn tokens.
+ * Unlike the reference it does not write -inf into the caller's logits. */
+int dlk_sample_grammar(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
+                       const uint32_t *off, const uint8_t *bytes, dlk_grammar_row *states, int eos_id,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -213,3 +213,64 @@ def test_apply_penalties_batched(cuda):
         got = d.cpu().numpy()
         for r in range(rows):
             np.testing.assert_array_equal(got[r], O.penalties(logits[r], hist[r], order, 1.2, 0.3, 0.5))
+
+
+@pytest.mark.parametrize("path", [0, 1])
+def test_sample_grammar_device_loop(cuda, path):
+    """dlk_sample_grammar for a number of steps -- each row's grammar mask, the
+    draw, and the row's state advanced by the drawn token, all on the device --
+    against the oracle's apply_mask -> sample -> advance sequence per row
+    (src/core/sampler_api.c:48-73), with the EOS rule and the rng carried on."""
+    import torch
+    L = _lib.lib()
+    rng = np.random.default_rng(21)
+    V = 3000
+    toks = random_vocab(rng, V)
+    strs = [t or b"" for t in toks]
+    off = np.zeros(V + 1, np.uint32)
+    off[1:] = np.cumsum([len(s) for s in strs])
+    data = np.frombuffer(b"".join(strs), np.uint8).copy()
+    eos = 9
+    modes = [b"receipt bbox_2d", b"root ::= object | value", b"free text", b"root ::= object | value"]
+    R, steps = len(modes), 16
+    T_, K_, P_ = 0.9, (0 if path == 0 else 40), 0.95
+    states = (_lib.GrammarRow * R)()
+    for i, mode in enumerate(modes):
+        L.dlk_grammar_row_init(C.byref(states[i]), L.dlk_grammar_mode_of(mode))
+    seeds = rng.integers(1, 2**63, R, dtype=np.uint64)
+    dev = torch.device("cuda:0")
+    d_off = torch.from_numpy(off.view(np.int32)).to(dev)
+    d_bytes = torch.from_numpy(data).to(dev)
+    d_states = torch.frombuffer(bytearray(bytes(states)), dtype=torch.uint8).to(dev)
+    d_rng = torch.from_numpy(seeds.view(np.int64).copy()).to(dev)
+    W_ = (V + 31) // 32
+    d_mask = torch.zeros((R, W_), dtype=torch.int32, device=dev)
+    d_out = torch.zeros(R, dtype=torch.int32, device=dev)
+    d_status = torch.zeros(1, dtype=torch.int32, device=dev)
+    prm = _lib.SampleParams(T_, K_, P_, 0.0, 1.0, 0.0, 0.0, _lib.ORDER_REFERENCE, 1, 0, path)
+    step_logits = [rng.normal(0, 2, (R, V)).astype(np.float32) for _ in range(steps)]
+    for lg in step_logits:
+        lg[:, :8] += 2.5                                        # the JSON pieces of random_vocab
+    got = np.zeros((steps, R), np.int32)
+    for s_ in range(steps):
+        d_lg = torch.from_numpy(step_logits[s_]).to(dev)
+        b = _lib.Batch(logits=d_lg.data_ptr(), ld=V, hist_off=None, hist_ids=None, mask=d_mask.data_ptr(), mask_ld=W_,
+                       mask_row=None, rng=d_rng.data_ptr(), out_ids=d_out.data_ptr(), out_cand_ids=None,
+                       out_cand_probs=None, out_cand_logprobs=None, status=d_status.data_ptr())
+        rc = L.dlk_sample_grammar(C.byref(b), R, V, C.byref(prm), d_off.data_ptr(), d_bytes.data_ptr(),
+                                  d_states.data_ptr(), eos, None)
+        assert rc == 0
+        got[s_] = d_out.cpu().numpy()
+    end_states = d_rng.cpu().numpy().view(np.uint64)
+    assert int(d_status.cpu().item()) == 0
+    for i, mode in enumerate(modes):
+        g = O.grammar(mode)
+        st = int(seeds[i])
+        for s_ in range(steps):
+            masked, _ = O.grammar_mask(g, off, data, eos, step_logits[s_][i])
+            o = O.sample_row(masked, st, T_, K_, P_, 0.0)
+            st = o["state"]
+            assert got[s_, i] == o["token"], (mode, s_, got[:, i], o["token"])
+            if o["token"] != eos and 0 <= o["token"] < V:
+                O.lib().orc_grammar_advance(C.byref(g), strs[o["token"]].split(b"\0")[0])
+        assert int(end_states[i]) == st
