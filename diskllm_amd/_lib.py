@@ -18,6 +18,7 @@ DLK_OK = 0
 DLK_ERR_INVALID = -1
 DLK_ERR_UNSUPPORTED = -2
 DLK_ERR_HIP = -3
+DLK_ERR_FORMAT = -4
 DLK_STATUS_HISTORY_TOO_LONG = 1
 PATH_AUTO, PATH_ROW, PATH_FULL_EXACT = 0, 1, 2
 
@@ -69,6 +70,7 @@ EXPORTS = [
     # include/diskllm_amd.h
     "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
     "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
+    "dlk_vocab_csr_from_gguf",
     # include/sampler.h
     "sampler_create", "sampler_free", "sampler_apply_repetition_penalty", "sampler_apply_presence_penalty",
     "sampler_sample", "greedy_sample",
@@ -123,6 +125,9 @@ def lib() -> C.CDLL:
         L.dlk_sample_grammar.restype = C.c_int
         L.dlk_sample_grammar.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p,
                                          C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        L.dlk_vocab_csr_from_gguf.restype = C.c_int
+        L.dlk_vocab_csr_from_gguf.argtypes = [C.c_char_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int64,
+                                              C.POINTER(C.c_int32), C.POINTER(C.c_int64)]
         # include/sampler.h
         L.sampler_create.restype = C.c_void_p
         L.sampler_create.argtypes = [C.POINTER(SamplerConfig)]
@@ -155,3 +160,19 @@ def lib() -> C.CDLL:
 def check(rc: int, what: str) -> None:
     if rc != DLK_OK:
         raise RuntimeError(f"{what} failed with status {rc}")
+
+
+def vocab_csr_from_gguf(path: str, vocab: int = 0):
+    """(off uint32[ids+1], bytes uint8[n], n_tokens) of a GGUF file's token
+    strings, through dlk_vocab_csr_from_gguf's sizing and filling calls."""
+    import numpy as np
+    L = lib()
+    nt, nb = C.c_int32(0), C.c_int64(0)
+    p = os.fsencode(path)
+    check(L.dlk_vocab_csr_from_gguf(p, vocab, None, None, 0, C.byref(nt), C.byref(nb)), "dlk_vocab_csr_from_gguf")
+    ids = vocab if vocab > 0 else nt.value
+    off = np.zeros(ids + 1, np.uint32)
+    data = np.zeros(max(nb.value, 1), np.uint8)
+    check(L.dlk_vocab_csr_from_gguf(p, vocab, off.ctypes.data, data.ctypes.data, data.size, C.byref(nt),
+                                    C.byref(nb)), "dlk_vocab_csr_from_gguf")
+    return off, data[:nb.value], nt.value

@@ -29,6 +29,7 @@ extern "C" {
 #define DLK_ERR_INVALID (-1)      /* bad argument */
 #define DLK_ERR_UNSUPPORTED (-2)  /* shape or parameter outside the supported range */
 #define DLK_ERR_HIP (-3)          /* a HIP runtime call failed */
+#define DLK_ERR_FORMAT (-4)       /* a file that cannot be opened, is truncated or is not in the format read */
 
 /* Device status bits written by the kernels (dlk_batch.status). */
 #define DLK_STATUS_HISTORY_TOO_LONG 1u  /* a row's history exceeded max_history: its id is -1 */
@@ -184,6 +185,22 @@ int dlk_grammar_advance(const uint32_t *off, const uint8_t *bytes, int vocab, dl
 int dlk_sample_grammar(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
                        const uint32_t *off, const uint8_t *bytes, dlk_grammar_row *states, int eos_id,
                        hipStream_t stream);
+
+/* The vocabulary table of the calls above (token t = bytes[off[t] .. off[t+1]),
+ * read up to its first NUL) from a GGUF file's `tokenizer.ggml.tokens` string
+ * array: the strings tokenizer_init loads (src/tokenizer.c:247-300) and
+ * tokenizer_decode_raw returns (src/tokenizer.c:377-380).  Host memory, no
+ * device work.  The table covers ids 0 .. vocab-1 (vocab <= 0: one id per
+ * string); ids past the file's strings get empty entries, which the mask
+ * disallows as the reference does the NULL string it gets for them.  A file
+ * with no tokens array gives an all-empty table (the reference's tokenizer
+ * has vocab_size 0 then).  Call once with off = NULL to get *n_tokens (the
+ * array's length) and *n_bytes (bytes the table needs), then with off
+ * ([vocab+1] entries) and bytes ([bytes_cap] bytes) to fill them.
+ * DLK_ERR_FORMAT: the file cannot be opened, is truncated, is not GGUF, or its
+ * tokens array does not hold strings; DLK_ERR_INVALID: bytes_cap too small. */
+int dlk_vocab_csr_from_gguf(const char *path, int vocab, uint32_t *off, uint8_t *bytes, int64_t bytes_cap,
+                            int32_t *n_tokens, int64_t *n_bytes);
 
 #ifdef __cplusplus
 }

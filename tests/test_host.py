@@ -5,6 +5,7 @@ reference compiled from its sources."""
 import ctypes as C
 import os
 import re
+import struct
 
 import numpy as np
 import pytest
@@ -150,3 +151,117 @@ def test_grammar_unit_kats_dropin():
     L.diskllm_grammar_advance(g, b'"bbox_2d": [123] }')
     assert L.diskllm_grammar_is_finished(g)
     L.diskllm_grammar_free(g)
+
+
+# --- vocabulary table from a GGUF file (dlk_vocab_csr_from_gguf) -------------------------------------------
+
+def _gguf_str(b: bytes) -> bytes:
+    return struct.pack("<Q", len(b)) + b
+
+
+def _gguf_value(t: int, v) -> bytes:
+    """One GGUF value of type t (the type ids and layouts of the GGUF format)."""
+    fmt = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+    if t in fmt:
+        return struct.pack(fmt[t], v)
+    if t == 8:
+        return _gguf_str(v)
+    et, items = v
+    return struct.pack("<IQ", et, len(items)) + b"".join(_gguf_value(et, x) for x in items)
+
+
+def _write_gguf(path, kvs, magic=b"GGUF"):
+    out = magic + struct.pack("<IQQ", 3, 0, len(kvs))
+    for key, t, v in kvs:
+        out += _gguf_str(key) + struct.pack("<I", t) + _gguf_value(t, v)
+    with open(path, "wb") as f:
+        f.write(out)
+    return out
+
+
+GGUF_TOKENS = [b"!", b"\"", b"{", b"}", "Ġthe".encode(), b"<0x0A>", b"", b"<|im_end|>", b"a\x00b",
+               "éè".encode(), b"[", b"]", b"12", b"\\", b" " * 300]
+# Every value type before the tokens, including strings, scalar arrays, string arrays and an array of
+# arrays, and a key that shares the tokens key's length.
+GGUF_PREFIX = [
+    (b"general.architecture", 8, b"qwen2"), (b"general.file_type", 4, 7), (b"a.u8", 0, 200), (b"a.i8", 1, -3),
+    (b"a.u16", 2, 65000), (b"a.i16", 3, -2), (b"a.i32", 5, -9), (b"a.f32", 6, 0.5), (b"a.bool", 7, True),
+    (b"a.u64", 10, 1 << 40), (b"a.i64", 11, -(1 << 40)), (b"a.f64", 12, 0.25),
+    (b"tokenizer.ggml.model", 8, b"gpt2"), (b"tokenizer.ggml.tokenz", 8, b"not the tokens"),
+    (b"tokenizer.ggml.scores", 9, (6, [0.5] * 7)), (b"tokenizer.ggml.token_type", 9, (5, [1, 2, 3])),
+    (b"a.nested", 9, (9, [(8, [b"x", b"yz"]), (4, [1, 2])])),
+]
+GGUF_SUFFIX = [(b"tokenizer.ggml.merges", 9, (8, ["Ġ t".encode(), b"h e"])), (b"tokenizer.ggml.eos_token_id", 4, 7)]
+
+
+def _ref_tokenizer():
+    path = os.path.join(ROOT, "oracle", "_ref", "libref_tokenizer.so")
+    if not os.path.exists(path):
+        return None
+    T = C.CDLL(path)
+    T.tokenizer_init.restype = C.c_void_p
+    T.tokenizer_init.argtypes = [C.c_char_p]
+    T.tokenizer_decode_raw.restype = C.c_void_p
+    T.tokenizer_decode_raw.argtypes = [C.c_void_p, C.c_int32]
+    T.tokenizer_free.argtypes = [C.c_void_p]
+    return T
+
+
+def _entries(off, data):
+    return [bytes(data[off[t]:off[t + 1]]) for t in range(len(off) - 1)]
+
+
+@pytest.mark.parametrize("vocab", [0, len(GGUF_TOKENS), 5, len(GGUF_TOKENS) + 9])
+def test_vocab_csr_from_gguf(tmp_path, vocab):
+    path = str(tmp_path / "v.gguf")
+    _write_gguf(path, GGUF_PREFIX + [(b"tokenizer.ggml.tokens", 9, (8, GGUF_TOKENS))] + GGUF_SUFFIX)
+    off, data, n = _lib.vocab_csr_from_gguf(path, vocab)
+    ids = vocab or len(GGUF_TOKENS)
+    assert n == len(GGUF_TOKENS) and len(off) == ids + 1 and off[0] == 0
+    want = (GGUF_TOKENS + [b""] * ids)[:ids]
+    assert _entries(off, data) == want
+    T = _ref_tokenizer()
+    if T is not None:                                   # the reference's own load of the same file
+        tok = T.tokenizer_init(path.encode())
+        assert tok
+        try:
+            for t in range(ids):
+                p = T.tokenizer_decode_raw(tok, t)
+                got = _entries(off, data)[t].split(b"\x00")[0]
+                assert (C.string_at(p) if p else b"") == got, t
+                assert (p is None) == (t >= len(GGUF_TOKENS)), t
+        finally:
+            T.tokenizer_free(tok)
+
+
+def test_vocab_csr_from_gguf_errors(tmp_path):
+    L = _lib.lib()
+    nt, nb = C.c_int32(-1), C.c_int64(-1)
+    full = _write_gguf(str(tmp_path / "ok.gguf"), GGUF_PREFIX + [(b"tokenizer.ggml.tokens", 9, (8, GGUF_TOKENS))])
+    call = lambda p, *a: L.dlk_vocab_csr_from_gguf(str(p).encode(), *a, C.byref(nt), C.byref(nb))
+    assert call(tmp_path / "missing.gguf", 0, None, None, 0) == _lib.DLK_ERR_FORMAT
+    _write_gguf(str(tmp_path / "magic.gguf"), GGUF_PREFIX, magic=b"GGUG")
+    assert call(tmp_path / "magic.gguf", 0, None, None, 0) == _lib.DLK_ERR_FORMAT
+    # Cut anywhere inside the metadata or the strings: a format error on both calls.
+    for cut in (3, 20, 100, len(full) // 2, len(full) - 301, len(full) - 1):
+        (tmp_path / "cut.gguf").write_bytes(full[:cut])
+        assert call(tmp_path / "cut.gguf", 0, None, None, 0) == _lib.DLK_ERR_FORMAT, cut
+        off, data = np.zeros(len(GGUF_TOKENS) + 1, np.uint32), np.zeros(4096, np.uint8)
+        assert call(tmp_path / "cut.gguf", len(GGUF_TOKENS), off.ctypes.data, data.ctypes.data,
+                    data.size) == _lib.DLK_ERR_FORMAT, cut
+    # Cut after the strings the table covers: only those are read.
+    (tmp_path / "cut.gguf").write_bytes(full[:len(full) - 308])
+    assert call(tmp_path / "cut.gguf", 5, None, None, 0) == _lib.DLK_OK and nt.value == len(GGUF_TOKENS)
+    # The tokens array holding something other than strings.
+    _write_gguf(str(tmp_path / "ints.gguf"), [(b"tokenizer.ggml.tokens", 9, (4, [1, 2, 3]))])
+    assert call(tmp_path / "ints.gguf", 0, None, None, 0) == _lib.DLK_ERR_FORMAT
+    # bytes_cap one short of what the sizing call reported.
+    assert call(tmp_path / "ok.gguf", 0, None, None, 0) == _lib.DLK_OK
+    need = nb.value
+    off, data = np.zeros(len(GGUF_TOKENS) + 1, np.uint32), np.zeros(need, np.uint8)
+    assert call(tmp_path / "ok.gguf", 0, off.ctypes.data, data.ctypes.data, need - 1) == _lib.DLK_ERR_INVALID
+    assert call(tmp_path / "ok.gguf", 0, off.ctypes.data, data.ctypes.data, need) == _lib.DLK_OK
+    # No tokens array: an all-empty table, as the reference's vocab_size 0 decodes nothing.
+    _write_gguf(str(tmp_path / "none.gguf"), GGUF_PREFIX)
+    off, data, n = _lib.vocab_csr_from_gguf(str(tmp_path / "none.gguf"), 6)
+    assert n == 0 and list(off) == [0] * 7 and data.size == 0
