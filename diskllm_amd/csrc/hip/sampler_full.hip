@@ -704,34 +704,54 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int cx = (x - s0) >> 6;
         Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + cp[min(nch, cx + 1)]);
     }
-    for (int c = t; c <= nch; c += T) Pc[c] = fmin(RWg + cp[c], Rx) * scale;
+    /* with each chunk's predicted binade: the binade of its start value when
+     * its end value has the same one, else kInvalidBinade */
+    for (int c = t; c <= nch; c += T) {
+        const double a = fmin(RWg + cp[c], Rx) * scale;
+        Pc[c] = a;
+        if (c < nch) {
+            const int bh = predict_binade<24>(a);
+            const bool valid = bh == predict_binade<24>(fmin(RWg + cp[c + 1], Rx) * scale) && bh >= -100;
+            cbh[c] = valid ? bh : kInvalidBinade;
+        }
+    }
     __syncthreads();
+    /* every lane reads its chunks' predicted binades before any is replaced: a
+     * chunk belongs to one 16-lane row of one wave, whose lane 15 replaces it
+     * below (all reads up front where the registers allow it) */
+    constexpr bool kPreload = EPT <= 40;
+    int pbh[EPT / 4];
+    if (kPreload) {
+#pragma unroll
+        for (int j4 = 0; j4 < EPT / 4; j4++) pbh[j4] = cbh[(t + j4 * T) >> 4];
+    }
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T;
         const int c = u >> 4;
-        const int bh = predict_binade<24>(Pc[c]);
-        const bool valid = bh == predict_binade<24>(Pc[c + 1]) && bh >= -100;
+        const int bh = kPreload ? pbh[j4] : cbh[c];
         /* the increments are integers below 2^24 wherever the prediction holds,
          * so their float sum is exact; where it does not the sum still reaches
          * 2^24 (non-negative terms, monotone rounding) and the walk opens the
          * chunk.  Computed for every lane (no branch: an invalid chunk's sum is
-         * not used); a tie saturates the lane's sum, so a chunk whose total
-         * reaches 2^24 -- a tie, or a sum that leaves the binade -- is opened. */
-        float fsum = 0.0f;
-        bool tie = false;
+         * not used, whatever its scale 2^(23 - kInvalidBinade) gives); a tie
+         * saturates the lane's sum, so a chunk whose total reaches 2^24 -- a
+         * tie, or a sum that leaves the binade -- is opened. */
+        float xs[4], n[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float xs = ldexpf(v[4 * j4 + k], 23 - bh);
-            const float n = rintf(xs);
-            tie |= fabsf(xs - n) == 0.5f;
-            fsum += n;
+            xs[k] = ldexpf(v[4 * j4 + k], 23 - bh);
+            n[k] = rintf(xs[k]);
         }
-        uint32_t sum = tie ? (1u << 25) : (uint32_t)fminf(fsum, 0x1p25f);
+        const float fsum = ((n[0] + n[1]) + n[2]) + n[3];
+        /* largest distance to the rounded value: 0.5 exactly iff one term is a tie */
+        const float fr = fmaxf(fmaxf(fabsf(xs[0] - n[0]), fabsf(xs[1] - n[1])),
+                               fmaxf(fabsf(xs[2] - n[2]), fabsf(xs[3] - n[3])));
+        uint32_t sum = fr == 0.5f ? (1u << 25) : (uint32_t)fminf(fsum, 0x1p25f);
         sum = row_scan_u32(sum);
         if ((lane & 15) == 15) {
             ca[c] = sum;
-            cbh[c] = (valid && sum < (1u << 24)) ? bh : kInvalidBinade;
+            cbh[c] = (bh != kInvalidBinade && sum < (1u << 24)) ? bh : kInvalidBinade;
         }
     }
     if (t == 0) misc[10] = 0;
@@ -748,11 +768,15 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const bool end = in && (!vld || c == nch - 1 || cbh[c + 1] != bc);
         const uint64_t a = vld ? (uint64_t)ca[c] : 0;
         const bool isel = in && !vld;
-        const uint32_t both = block_excl_prefix_u32((end ? 1u : 0u) | (isel ? 0x10000u : 0u), (uint32_t *)L.bi);
-        const uint32_t run = both & 0xffffu;
-        if (isel) elpos = (int)(both >> 16);
-        if (t == T - 1) misc[17] = (int)(both >> 16) + (isel ? 1 : 0);
-        const uint64_t ainc = block_incl_prefix_u64(a, (uint64_t *)L.red);
+        /* one scan of three fields: increments (below 2^24 per chunk, so below
+         * 2^34 in all), run ends (bits 40-51) and element-level chunks (52-63),
+         * the counts at most nch <= 4095 */
+        const uint64_t all = block_incl_prefix_u64(a | ((uint64_t)end << 40) | ((uint64_t)isel << 52),
+                                                   (uint64_t *)L.red);
+        const uint64_t ainc = all & ((1ull << 40) - 1);
+        const uint32_t run = (uint32_t)((all >> 40) & 0xfffu) - (end ? 1u : 0u);
+        if (isel) elpos = (int)(all >> 52) - 1;
+        if (t == T - 1) misc[17] = (int)(all >> 52);
         if (end) { rend[run] = c; rpre[run] = ainc; }
         __syncthreads();
         if (in) {
