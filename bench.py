@@ -86,6 +86,8 @@ def other_bytes(w) -> int:
     import numpy as np
     V, rows = w.vocab, w.rows
     W = (V + 31) // 32
+    if getattr(w, "epilogue", False):
+        return rows * V * 8                              # each logit read and written once
     if w.name == "C4":
         csr = (V + 1) * 4 + int(w.dfa.data.size) + int(w.dfa.trans.size)
         return csr + rows * (4 + W * 4)                 # CSR + table once, a state in and a mask row out per row
@@ -111,7 +113,24 @@ def run_other(name: str, args) -> int:
     w = workloads.CONFIGS[name]()
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    if name == "C4":
+    if name == "C5CAP":
+        from diskllm_amd import _lib
+        w.epilogue = True
+        cap = workloads.CAP_C5CAP
+        lg = api._dev(np.ascontiguousarray(w.logits), dev)
+
+        def step():
+            _lib.check(_lib.lib().dlk_softcap(lg.data_ptr(), w.vocab, w.rows, w.vocab, cap, sh), "dlk_softcap")
+        step()
+        torch.cuda.synchronize()
+        got = lg.cpu().numpy()
+        check = list(range(min(w.rows, 32)))
+        want = np.ascontiguousarray(w.logits[check])
+        O.lib().orc_softcap(want.reshape(-1), want.reshape(-1), want.size, np.float32(cap))
+        n_ok = sum(int(np.array_equal(got[r].view(np.uint32), want[r].view(np.uint32))) for r in check)
+        parity = f"{n_ok}/{len(check)} capped rows bit-identical to the oracle (rows 0..{len(check) - 1})"
+        # the timed steps re-cap the capped rows in place: the same work per element
+    elif name == "C4":
         d = w.dfa
         t_off = api._dev(np.asarray(d.offsets, np.uint32), dev)
         t_dat = api._dev(np.asarray(d.data, np.uint8), dev)
@@ -173,6 +192,8 @@ def run_other(name: str, args) -> int:
                      "ms_per_launch": round(ms_dev, 5)},
         "cpu_baseline": None,
     }
+    if name == "C5CAP":
+        line["roofline"]["kernel"] = "dlk::softcap_vec_kernel"
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_other(w, args.cpu_runs)
     print(json.dumps(line), flush=True)
@@ -186,6 +207,20 @@ def cpu_other(w, runs: int) -> dict:
     import numpy as np
     from oracle import oracle as O
     nthreads = min(16, os.cpu_count() or 1)
+    if getattr(w, "epilogue", False):
+        rows = min(w.rows, 32)
+        x = np.ascontiguousarray(w.logits[:rows]).reshape(-1)
+        y = np.empty_like(x)
+        ts = []
+        for _ in range(max(1, runs // 4)):
+            t0 = time.perf_counter()
+            O.lib().orc_softcap(x, y, x.size, np.float32(30.0))
+            ts.append(time.perf_counter() - t0)
+        sec = float(np.median(ts))
+        return {"value": round(rows / sec, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"rows 0..{rows - 1}, the reference's loop cap * tanhf(x / cap) with the host libm "
+                          f"(oracle/oracle.c orc_softcap; one thread, as in src/core/context.c:873-876), "
+                          f"median of {len(ts)} passes"}
     if w.name == "C4":
         t0 = time.perf_counter()
         for r in range(w.rows):
@@ -245,7 +280,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP"],
                     help="C2 (default) is the headline line; the others are the scope table's parity "
                          "configurations, measured the same way")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

@@ -70,7 +70,7 @@ EXPORTS = [
     # include/diskllm_amd.h
     "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
     "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
-    "dlk_vocab_csr_from_gguf",
+    "dlk_vocab_csr_from_gguf", "dlk_softcap",
     # include/sampler.h
     "sampler_create", "sampler_free", "sampler_apply_repetition_penalty", "sampler_apply_presence_penalty",
     "sampler_sample", "greedy_sample",
@@ -125,6 +125,8 @@ def lib() -> C.CDLL:
         L.dlk_sample_grammar.restype = C.c_int
         L.dlk_sample_grammar.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p,
                                          C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        L.dlk_softcap.restype = C.c_int
+        L.dlk_softcap.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_float, C.c_void_p]
         L.dlk_vocab_csr_from_gguf.restype = C.c_int
         L.dlk_vocab_csr_from_gguf.argtypes = [C.c_char_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int64,
                                               C.POINTER(C.c_int32), C.POINTER(C.c_int64)]

@@ -190,4 +190,12 @@ def c5(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
                     dfa=DFA(off, data, trans), dfa_states=states, n_out=20)
 
 
-CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C4": c4, "C5": c5}
+def c5cap(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
+    """The reference's decode epilogue on C5's logits: soft-cap cap * tanhf(x / cap)
+    with cap 30 (the Gemma final-logit cap), in place, 512 x 262144 fp32."""
+    return c5(seed, rows, vocab)
+
+
+CAP_C5CAP = 30.0
+
+CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C4": c4, "C5": c5, "C5CAP": c5cap}

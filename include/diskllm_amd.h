@@ -186,6 +186,12 @@ int dlk_sample_grammar(const dlk_batch *batch, int rows, int vocab, const dlk_sa
                        const uint32_t *off, const uint8_t *bytes, dlk_grammar_row *states, int eos_id,
                        hipStream_t stream);
 
+/* The reference's logit soft-cap, in place: logits[r * ld + i] = cap *
+ * tanhf(logits[r * ld + i] / cap) for i < vocab (src/core/context.c:604-606
+ * after a prefill, :873-876 after a decode step, a host loop there), with tanhf
+ * bit-identical to the host libm's.  No-op unless cap > 0, as in the reference. */
+int dlk_softcap(float *logits, int64_t ld, int rows, int vocab, float cap, hipStream_t stream);
+
 /* The vocabulary table of the calls above (token t = bytes[off[t] .. off[t+1]),
  * read up to its first NUL) from a GGUF file's `tokenizer.ggml.tokens` string
  * array: the strings tokenizer_init loads (src/tokenizer.c:247-300) and

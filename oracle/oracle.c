@@ -457,3 +457,44 @@ void orc_expf_bits(uint32_t first, long n, float *out, int threads) {
     }
     for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
 }
+
+/* The reference's logit soft-cap (src/core/context.c:604-606 and :873-876):
+ * y[i] = cap * tanhf(x[i] / cap) with the host libm, applied only when cap > 0;
+ * y may equal x. */
+void orc_softcap(const float *x, float *y, long n, float cap) {
+    if (!(cap > 0.0f)) {
+        if (y != x) memmove(y, x, (size_t)n * sizeof(float));
+        return;
+    }
+    for (long i = 0; i < n; i++) y[i] = cap * tanhf(x[i] / cap);
+}
+
+typedef struct { uint32_t first; long n; float *out; } orc_tanhf_job;
+
+static void *orc_tanhf_worker(void *arg) {
+    orc_tanhf_job *j = (orc_tanhf_job *)arg;
+    for (long i = 0; i < j->n; i++) {
+        uint32_t u = j->first + (uint32_t)i;
+        float x;
+        memcpy(&x, &u, 4);
+        j->out[i] = tanhf(x);
+    }
+    return NULL;
+}
+
+/* out[i] = tanhf(bits(first + i)) with the host libm, over `threads` threads. */
+void orc_tanhf_bits(uint32_t first, long n, float *out, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t th[64];
+    orc_tanhf_job jobs[64];
+    long per = (n + threads - 1) / threads;
+    for (int t = 0; t < threads; t++) {
+        long a = t * per, b = a + per < n ? a + per : n;
+        jobs[t].first = first + (uint32_t)(a > n ? n : a);
+        jobs[t].n = b > a ? b - a : 0;
+        jobs[t].out = out + (a > n ? n : a);
+        pthread_create(&th[t], NULL, orc_tanhf_worker, &jobs[t]);
+    }
+    for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+}

@@ -54,4 +54,6 @@ bool orc_grammar_finished(const orc_grammar *g);
 int orc_grammar_mask(const orc_grammar *g, float *logits, int vocab, const uint32_t *off,
                      const uint8_t *bytes, int eos_id);
 void orc_expf_bits(uint32_t first, long n, float *out, int threads);
+void orc_softcap(const float *x, float *y, long n, float cap);
+void orc_tanhf_bits(uint32_t first, long n, float *out, int threads);
 #endif

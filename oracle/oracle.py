@@ -83,6 +83,8 @@ def lib() -> C.CDLL:
         L.orc_json_prefix.restype = C.c_bool
         L.orc_json_prefix.argtypes = [C.c_char_p, C.c_int]
         L.orc_expf_bits.argtypes = [C.c_uint32, C.c_long, _f32p, C.c_int]
+        L.orc_softcap.argtypes = [_f32p, _f32p, C.c_long, C.c_float]
+        L.orc_tanhf_bits.argtypes = [C.c_uint32, C.c_long, _f32p, C.c_int]
         L.orc_grammar_init.argtypes = [C.POINTER(OrcGrammar), C.c_char_p]
         L.orc_grammar_accept.restype = C.c_bool
         L.orc_grammar_accept.argtypes = [C.POINTER(OrcGrammar), C.c_char_p]

@@ -151,3 +151,78 @@ def test_c5_gemma_dfa_topk(cuda, path):
     _announce(f"C5 rows={w.rows} V={w.vocab} path={path}")
     res = run_gpu(w, path=path)
     assert_rows_match(w, res, list(range(w.rows)))
+
+
+def test_device_tanhf_exhaustive(cuda):
+    """dlk_softcap with cap 1 (1 * tanhf(x / 1) = tanhf(x) bit for bit) == host libm
+    tanhf on every non-NaN float (2^32 inputs, 2^26 per slice)."""
+    import torch
+    from diskllm_amd import _lib
+    _announce("tanhf exhaustive through dlk_softcap(cap=1), 64 slices of 2^26")
+    n = 1 << 26
+    xs = torch.empty(n, dtype=torch.int32, device="cuda")
+    host = np.empty(n, np.float32)
+    base = torch.arange(n, dtype=torch.int64, device="cuda")
+    bad_total = 0
+    for s in range(64):
+        first = s * n
+        v = base + first
+        xs.copy_(torch.where(v >= 2 ** 31, v - 2 ** 32, v).to(torch.int32))
+        _lib.check(_lib.lib().dlk_softcap(xs.data_ptr(), n, 1, n, 1.0, torch.cuda.current_stream().cuda_stream),
+                   "dlk_softcap")
+        O.lib().orc_tanhf_bits(first, n, host, 16)
+        g = xs.cpu().numpy().view(np.uint32)
+        h = host.view(np.uint32)
+        xin = (np.arange(n, dtype=np.uint64) + first).astype(np.uint32)
+        nan_in = ((xin & 0x7F800000) == 0x7F800000) & ((xin & 0x007FFFFF) != 0)
+        bad = np.nonzero((g != h) & ~nan_in)[0]
+        if bad.size:
+            print("mismatch", hex(int(xin[bad[0]])), hex(int(g[bad[0]])), hex(int(h[bad[0]])))
+        bad_total += bad.size
+    assert bad_total == 0
+
+
+@pytest.mark.parametrize("rows,vocab,ld,offset,cap", [(3, 262144, 262144, 0, 30.0), (5, 1001, 1003, 1, 30.0),
+                                                      (2, 151936, 152000, 0, 50.0), (1, 7, 7, 3, 0.5),
+                                                      (4, 4096, 4100, 0, 0.0)])
+def test_softcap_rows_vs_oracle(cuda, rows, vocab, ld, offset, cap):
+    """dlk_softcap over strided rows (float4 and scalar paths, ragged tails) ==
+    the oracle's cap * tanhf(x / cap), bit for bit; the padding past vocab and
+    the rows for cap <= 0 are left alone."""
+    import torch
+    from diskllm_amd import _lib
+    _announce(f"softcap rows={rows} vocab={vocab} ld={ld} offset={offset} cap={cap}")
+    rng = np.random.default_rng(vocab + rows)
+    buf = rng.normal(0.0, 40.0, size=rows * ld + offset).astype(np.float32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 1e-38, -1e-45, 22.0 * 30, 3.4e38, -3.4e38], np.float32)
+    buf[offset:offset + min(special.size, vocab)] = special[:vocab]
+    d = torch.from_numpy(buf.copy()).cuda()
+    _lib.check(_lib.lib().dlk_softcap(d.data_ptr() + 4 * offset, ld, rows, vocab, cap,
+                                      torch.cuda.current_stream().cuda_stream), "dlk_softcap")
+    got = d.cpu().numpy()
+    want = buf.copy()
+    for r in range(rows):
+        seg = want[offset + r * ld: offset + r * ld + vocab]
+        O.lib().orc_softcap(seg, seg, vocab, np.float32(cap))
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("path", [0, 1])
+def test_softcap_then_sample_vs_oracle(cuda, path):
+    """The reference's decode epilogue order on the device: soft-cap (cap 30, the
+    Gemma value) in place, then the C5 sampling step (DFA mask, repetition
+    penalty, top-k 64, top-p 0.95) on 48 rows; token ids and rng states equal to
+    the oracle's on the capped logits."""
+    from diskllm_amd import api, _lib
+    import torch
+    w = W.c5(rows=48)
+    _announce(f"softcap 30 -> C5 rows={w.rows} V={w.vocab} path={path}")
+    db = api.to_device(w)
+    _lib.check(_lib.lib().dlk_softcap(db.logits.data_ptr(), w.vocab, w.rows, w.vocab, 30.0,
+                                      torch.cuda.current_stream().cuda_stream), "dlk_softcap")
+    api.sample(db, api.params_of(w, path=path))
+    res = api.results(db)
+    capped = w.logits.copy()
+    O.lib().orc_softcap(capped.reshape(-1), capped.reshape(-1), capped.size, np.float32(30.0))
+    w.logits = capped
+    assert_rows_match(w, res, list(range(w.rows)))

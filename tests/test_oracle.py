@@ -444,3 +444,38 @@ def test_sample_nan_and_inf_rows_vs_reference():
                 tok, st_ref, _, _ = O.ref_sample_row("strict", row, st, T, k, p, 0.0)
                 o = O.sample_row(row, st, T, k, p, 0.0)
                 assert (o["token"], o["state"]) == (tok, st_ref), (V, T, k, p, case, o["token"], tok)
+
+
+# ------------------------------------------------------------------------ tanhf / soft-cap
+
+def test_tanhf_restatement_vs_host_libm():
+    """The device tanhf (diskllm_amd/csrc/hip/tanhf_glibc.h) compiled for the host,
+    against this host's libm tanhf, on every 1031st float bit pattern, and the
+    soft-cap cap * tanhf(x / cap) for the Gemma cap 30 and two others (the
+    exhaustive run is the same program with stride 1: 4,278,190,082 inputs, 0
+    mismatches)."""
+    exe = os.path.join(ROOT, "oracle", "_build", "tanhf_host_check")
+    src = os.path.join(ROOT, "tests", "native", "tanhf_host_check.c")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm", "-lpthread"], check=True)
+    for extra, stride in (([], 1031), (["cap=30"], 2053), (["cap=0.75"], 4099), (["cap=1e4"], 4099)):
+        r = subprocess.run([exe, "0", str(1 << 32), str(stride), "8"] + extra, capture_output=True, text=True,
+                           timeout=300)
+        checked, bad = map(int, r.stdout.split())
+        assert checked > 1000000 and bad == 0, (extra, r.stdout, r.stderr[:500])
+
+
+def test_oracle_softcap_known_values():
+    """orc_softcap against values fixed by the mathematics: tanh(0) = 0 (sign
+    kept), tanh saturates to +-1 at |x| >= 22 (so cap * 1 = cap), tanh(x) ~ x
+    near 0, odd symmetry, no-op for cap <= 0 or NaN."""
+    x = np.array([0.0, -0.0, 1e-30, 22.0 * 30, -1e30, np.inf, -np.inf, 15.0, -15.0, 3.0], np.float32)
+    y = np.empty_like(x)
+    O.lib().orc_softcap(x, y, x.size, np.float32(30.0))
+    assert y[0] == 0.0 and not np.signbit(y[0]) and y[1] == 0.0 and np.signbit(y[1])
+    assert y[2] == np.float32(1e-30)
+    assert y[3] == 30.0 and y[4] == -30.0 and y[5] == 30.0 and y[6] == -30.0
+    assert y[7] == -y[8]
+    assert abs(float(y[9]) - 30.0 * np.tanh(0.1)) < 1e-5
+    for cap in (0.0, -1.0, np.nan):
+        O.lib().orc_softcap(x, y, x.size, np.float32(cap))
+        np.testing.assert_array_equal(y.view(np.uint32), x.view(np.uint32))
