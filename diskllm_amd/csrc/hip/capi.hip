@@ -112,7 +112,11 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
         if ((int64_t)g * KP > 4096 || 4 * g + 2 > T) break;
         ept = e;
         G = g;
-        if ((int64_t)rows * g >= 1024) break;
+        /* the largest slices that still give one workgroup per CU: more, shorter
+         * workgroups add merge work faster than they add memory parallelism
+         * (32 x 151,936, top-k 50: 8 elements per thread 64 us, 16 or 32 48 us;
+         * 512 x 262,144, top-k 64: 64 per thread 538 us, 32 767 us) */
+        if ((int64_t)rows * g >= 256) break;
     }
     if (G == 0 || 4 * G + 2 > T) return 1;
     TopkParams f;
