@@ -129,6 +129,26 @@ __device__ __forceinline__ void bitonic_sort(K *a, int n) {
     }
 }
 
+/* Ascending sort of n <= blockDim.x distinct 64-bit keys a[0..n) in LDS, by
+ * rank: thread i counts the keys below a[i] (broadcast reads, no barrier per
+ * step) and stores a[i] at that position.  Two barriers, where a bitonic network
+ * over the next power of two takes one per pass.  Keys at and past n are not
+ * touched. */
+template <class K>
+__device__ __forceinline__ void rank_sort_distinct(K *a, int n) {
+    const int i = threadIdx.x;
+    K key = K();
+    int r = 0;
+    if (i < n) {
+        key = a[i];
+#pragma unroll 8
+        for (int j = 0; j < n; j++) r += a[j] < key ? 1 : 0;
+    }
+    __syncthreads();
+    if (i < n) a[r] = key;
+    __syncthreads();
+}
+
 /* The key of rank r (0-based, ascending) among the n 32-bit keys key(i),
  * i < n, 0 <= r < n: four rounds of 8-bit digits over an LDS histogram of 256
  * counters (hist) and two broadcast words (bc); a handful of barriers where a

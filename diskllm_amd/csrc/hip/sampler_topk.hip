@@ -204,7 +204,9 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
             while (P < C) P <<= 1;
             for (int i = C + t; i < P; i += T) buf[i] = ~0ull;
             __syncthreads();
-            bitonic_sort(buf, P);
+            /* keys carry their index: distinct, so a rank sort when they fit */
+            if (C <= T) rank_sort_distinct(buf, C);
+            else bitonic_sort(buf, P);
             kept = min(KP, C);
             complete = (C == nf) ? 1 : 0;
             last_key = (uint32_t)(buf[kept - 1] >> 32);
@@ -386,7 +388,8 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         while (P < nsort) P <<= 1;
         for (int i = nsort + t; i < P; i += T) buf[i] = ~0ull;
         __syncthreads();
-        bitonic_sort(buf, P);
+        if (nsort <= T) rank_sort_distinct(buf, nsort);
+        else bitonic_sort(buf, P);
         if (NF >= k) {
             /* certify: every slice that kept only part of its finite elements
              * must have its last kept candidate strictly below the k-th s */
