@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kSoftcapThreads) void softcap_scalar_kernel(float *
 
 extern "C" int dlk_softcap(float *logits, int64_t ld, int rows, int vocab, float cap, hipStream_t stream) {
     if (!logits || rows < 0 || vocab < 0 || ld < vocab) return DLK_ERR_INVALID;
-    if (rows > 65535) return DLK_ERR_UNSUPPORTED;
+    if (rows > 65535 || vocab > 0x7fffffff - 8192) return DLK_ERR_UNSUPPORTED;   /* grid rows; int indices */
     /* the reference caps only when the model's cap is positive (a NaN cap too is no cap) */
     if (rows == 0 || vocab == 0 || !(cap > 0.0f)) return DLK_OK;
     const bool vec = ld % 4 == 0 && ((uintptr_t)logits & 15u) == 0;
