@@ -265,3 +265,19 @@ def test_vocab_csr_from_gguf_errors(tmp_path):
     _write_gguf(str(tmp_path / "none.gguf"), GGUF_PREFIX)
     off, data, n = _lib.vocab_csr_from_gguf(str(tmp_path / "none.gguf"), 6)
     assert n == 0 and list(off) == [0] * 7 and data.size == 0
+
+
+def test_softcap_argument_checks():
+    """dlk_softcap's host-side checks (no device work is started by any of these):
+    bad pointers and shapes are DLK_ERR_INVALID, a grid beyond the row limit is
+    DLK_ERR_UNSUPPORTED, and cap <= 0 or NaN is the reference's no-op."""
+    L = _lib.lib()
+    fake = C.c_void_p(16)                     # never dereferenced: every call below returns first
+    assert L.dlk_softcap(None, 8, 1, 8, 30.0, None) == _lib.DLK_ERR_INVALID
+    assert L.dlk_softcap(fake, 7, 1, 8, 30.0, None) == _lib.DLK_ERR_INVALID          # ld < vocab
+    assert L.dlk_softcap(fake, 8, -1, 8, 30.0, None) == _lib.DLK_ERR_INVALID
+    assert L.dlk_softcap(fake, 8, 1, -1, 30.0, None) == _lib.DLK_ERR_INVALID
+    assert L.dlk_softcap(fake, 8, 70000, 8, 30.0, None) == _lib.DLK_ERR_UNSUPPORTED
+    for cap in (0.0, -3.0, float("nan")):
+        assert L.dlk_softcap(fake, 8, 4, 8, cap, None) == _lib.DLK_OK
+    assert L.dlk_softcap(fake, 8, 0, 8, 30.0, None) == _lib.DLK_OK
