@@ -57,6 +57,15 @@ def profiled_traffic(kernel: str):
     return None
 
 
+def host_threads() -> int:
+    """Host threads the CPU baseline may use: the CPUs this process may run on
+    (the GPU box gives one GPU 16 of them)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(w, runs: int, threads_all: int, kind: str = "strict") -> dict:
     """The reference src/sampler.c (strict ISO C build in oracle/_ref, or with
     kind "fast" the reference Makefile's -O3 -ffast-math build) on the host:
@@ -153,9 +162,26 @@ def run_other(name: str, args) -> int:
     else:
         db = api.to_device(w, device=dev)
         params = api.params_of(w)
+        if w.dfa is not None:
+            # C5: the step includes the DFA pass, one mask row per DFA state (the rows
+            # then pick theirs through mask_row), rebuilt into db.mask every step
+            from diskllm_amd import _lib
+            d = w.dfa
+            t_off = api._dev(np.asarray(d.offsets, np.uint32), dev)
+            t_dat = api._dev(np.asarray(d.data, np.uint8), dev)
+            t_tr = api._dev(np.ascontiguousarray(d.trans, np.uint8), dev)
+            n_st = d.trans.shape[0]
+            t_all = api._dev(np.arange(n_st, dtype=np.int32), dev)
+            W = db.mask.shape[1]
 
-        def step():
-            api.sample(db, params, sh)
+            def step():
+                _lib.check(_lib.lib().dlk_dfa_mask(t_off.data_ptr(), t_dat.data_ptr(), w.vocab, t_tr.data_ptr(), n_st,
+                                                   t_all.data_ptr(), n_st, d.eos_id, d.accept & 0xFFFFFFFFFFFFFFFF,
+                                                   db.mask.data_ptr(), W, sh), "dlk_dfa_mask")
+                api.sample(db, params, sh)
+        else:
+            def step():
+                api.sample(db, params, sh)
         step()
         res = api.results(db)
         check = list(range(min(w.rows, 32)))
@@ -194,6 +220,9 @@ def run_other(name: str, args) -> int:
     }
     if name == "C5CAP":
         line["roofline"]["kernel"] = "dlk::softcap_vec_kernel"
+    if w.dfa is not None and name != "C4":
+        line["config"]["step"] = ("dlk_dfa_mask over every DFA state (the mask table, rebuilt inside each timed "
+                                  "step), then one dlk_sample call whose rows pick their state's mask row")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_other(w, args.cpu_runs)
     print(json.dumps(line), flush=True)
@@ -206,7 +235,7 @@ def cpu_other(w, runs: int) -> dict:
     mask has no counterpart in the reference); C5 both, on a 32-row sample."""
     import numpy as np
     from oracle import oracle as O
-    nthreads = min(16, os.cpu_count() or 1)
+    nthreads = host_threads()
     if getattr(w, "epilogue", False):
         rows = min(w.rows, 32)
         x = np.ascontiguousarray(w.logits[:rows]).reshape(-1)
@@ -293,6 +322,14 @@ def main() -> int:
               "(row sharding) is not part of this build; run with --gpus 1", file=sys.stderr)
         return 2
 
+    maps_out = os.environ.get("DLK_EXIT_MAPS")
+    if maps_out:
+        # the process's mappings as the interpreter begins to exit, so that frames
+        # of a fault in a library's exit handler can be matched to their library
+        import atexit
+        import shutil
+        atexit.register(lambda: shutil.copyfile("/proc/self/maps", maps_out))
+
     import numpy as np
     import torch
     from diskllm_amd import api, workloads
@@ -366,7 +403,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu:
-        nthreads = min(16, os.cpu_count() or 1)
+        nthreads = host_threads()
         cb = cpu_baseline(w, args.cpu_runs, nthreads)
         if cb is not None:
             top = cb[max(cb)]
@@ -374,7 +411,8 @@ def main() -> int:
                 "value": round(top["value"], 1), "unit": "rows/s", "cores": max(cb), "kind": "reference",
                 "sample": f"full C2 batch (64 rows), median of {args.cpu_runs} runs, strict -std=c11 -O2 build",
                 "single_thread": round(cb[1]["value"], 1),
-                "ids_match_gpu": bool(np.array_equal(top["ids"], orc["ids"])),
+                # the reference build's ids against the GPU's first-step ids (same seeds)
+                "ids_match_gpu": bool(np.array_equal(top["ids"], res["ids"])),
             }
             fast = cpu_baseline(w, args.cpu_runs, nthreads, "fast")
             if fast is not None:

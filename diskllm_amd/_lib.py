@@ -82,9 +82,10 @@ EXPORTS = [
 
 
 def build(quiet: bool = True) -> None:
-    """Compile every HIP source for gfx950 and link the shared library in-tree."""
-    jobs = str(min(16, os.cpu_count() or 4))
-    r = subprocess.run(["make", "-C", CSRC, "-j", jobs], capture_output=True, text=True)
+    """Compile every HIP source for gfx950 and link the shared library in-tree
+    (always from scratch: every call compiles, also over an existing build)."""
+    jobs = str(min(16, len(os.sched_getaffinity(0)) or 4))
+    r = subprocess.run(["make", "-B", "-C", CSRC, "-j", jobs], capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("libdiskllm_amd build failed:\n" + r.stdout[-4000:] + r.stderr[-8000:])
     if not quiet:

@@ -18,11 +18,11 @@
  *   - orc_rand_f32 / xorshift: closed form + differential vs oracle/_ref build.
  *   - orc_greedy, penalties: closed form per id + differential vs oracle/_ref.
  *   - orc_sample: differential vs the reference src/sampler.c compiled from its own
- *     sources into oracle/_ref (tests/test_oracle_ref.py), plus invariants.
+ *     sources into oracle/_ref (tests/test_oracle.py), plus invariants.
  *   - grammar validators: the reference KATs (tools/test_grammar_unit.c:17-24)
  *     and differential vs the reference grammar.c compiled into oracle/_ref.
  *   - DFA mask: no reference counterpart; pinned by an independent numpy walk
- *     (tests/test_oracle_dfa.py) and hand-built tiny DFAs.
+ *     (tests/test_oracle.py) and hand-built tiny DFAs.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <math.h>

@@ -184,7 +184,9 @@ def test_device_tanhf_exhaustive(cuda):
 
 @pytest.mark.parametrize("rows,vocab,ld,offset,cap", [(3, 262144, 262144, 0, 30.0), (5, 1001, 1003, 1, 30.0),
                                                       (2, 151936, 152000, 0, 50.0), (1, 7, 7, 3, 0.5),
-                                                      (4, 4096, 4100, 0, 0.0)])
+                                                      (4, 4096, 4100, 0, 0.0),
+                                                      # float4 path (ld % 4 == 0, aligned) with ragged row ends
+                                                      (2, 1001, 1004, 0, 30.0), (1, 151937, 151940, 0, 30.0)])
 def test_softcap_rows_vs_oracle(cuda, rows, vocab, ld, offset, cap):
     """dlk_softcap over strided rows (float4 and scalar paths, ragged tails) ==
     the oracle's cap * tanhf(x / cap), bit for bit; the padding past vocab and
