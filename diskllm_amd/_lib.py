@@ -20,6 +20,8 @@ DLK_ERR_UNSUPPORTED = -2
 DLK_ERR_HIP = -3
 DLK_ERR_FORMAT = -4
 DLK_STATUS_HISTORY_TOO_LONG = 1
+DLK_STATUS_SYNC_TIMEOUT = 2
+DLK_STATUS_UNSUPPORTED_ROW = 4
 PATH_AUTO, PATH_ROW, PATH_FULL_EXACT = 0, 1, 2
 
 OP_REPETITION, OP_FREQUENCY, OP_PRESENCE = 1, 2, 3
@@ -31,7 +33,7 @@ class SampleParams(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
                 ("repeat_penalty", C.c_float), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float),
                 ("penalty_order", C.c_uint32), ("max_history", C.c_int), ("n_out", C.c_int),
-                ("path", C.c_int)]
+                ("path", C.c_int), ("softcap", C.c_float)]
 
 
 class Batch(C.Structure):

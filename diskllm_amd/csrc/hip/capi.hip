@@ -1,7 +1,7 @@
 /*
  * capi.hip -- host side of the batched C ABI (include/diskllm_amd.h): argument
  * checks, the scalars the reference computes on the host side of its loops
- * (1/temperature, the top-p threshold), LDS planning and the launch.
+ * (1/temperature, the top-p threshold), LDS planning, workspace and the launch.
  */
 #include <math.h>
 #include <string.h>
@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <vector>
 
 #include "sampler_params.h"
 #include "sampler_topk.h"
@@ -18,11 +19,17 @@ extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t l
 extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 extern "C" int dlk_full_kernel_capacity(int ept, size_t lds);
+extern "C" int dlk_launch_prepare_rows(const float *src, int64_t ld, float *dst, int64_t dld, int rows, int vocab,
+                                       const uint32_t *mask, int64_t mask_ld, const int32_t *mask_row, float cap,
+                                       hipStream_t stream);
 
 namespace {
 
 constexpr size_t kMaxLds = 160 * 1024;
-constexpr int kMaxTopK = 4096;
+constexpr int kMaxTopKLds = 4096;          /* larger top-k: candidates in global memory */
+constexpr int kHcapDirect = 1024;          /* longer histories: penalties applied to a scratch copy first */
+constexpr size_t kGlobalTopkBudget = (size_t)256 << 20;   /* workspace per launch of the large-k row kernel */
+constexpr int kLsdWords = 256 + 16 * 256 + 16;            /* select_top_k_global's LDS words */
 
 size_t r16(size_t b) { return (b + 15) & ~(size_t)15; }
 
@@ -46,53 +53,84 @@ double topp_threshold(float tp) {
     return nextafter(mid, INFINITY);
 }
 
-/* One lazily grown workspace per device: a zero-initialised counter region that
- * only the kernels' counter protocol writes (each counter is back at zero when a
- * launch finishes), then a scratch region.  Calls that overlap on one device must
- * not share it (use one stream). */
-struct DeviceWorkspace {
-    void *ptr = nullptr;
-    size_t ctr_cap = 0;     /* counters */
-    size_t data_bytes = 0;  /* scratch bytes after the counters */
+/* ---- workspace --------------------------------------------------------------
+ * Device scratch of the kernels, one lazily grown buffer per (device, stream,
+ * kind): kernels queued on one stream run in order, so they may share it, and
+ * calls on different streams never do.  Kind 0 starts with a counter region
+ * that is zero between launches (each launch returns its counters to zero),
+ * then scratch; kind 1 holds the prepared logits of dlk_sample's pre-pass.
+ * g_mu guards the table and is held by each entry point from its first
+ * workspace() through its last launch, so no buffer is regrown (freed) between
+ * the moment a call takes its pointers and the moment its kernels are queued. */
+struct WsBuf {
+    int dev;
+    hipStream_t stream;
+    int kind;
+    void *ptr;
+    size_t ctr_cap;      /* counter words */
+    size_t data_bytes;   /* scratch bytes after the counters */
 };
-std::mutex g_ws_mu;
-DeviceWorkspace g_ws[64];
+std::mutex g_mu;
+std::vector<WsBuf> g_ws;
 
 struct WsView {
     uint32_t *counters;
     unsigned char *data;
 };
 
-bool workspace(size_t counters, size_t data_bytes, WsView &out) {
+bool workspace(hipStream_t stream, int kind, size_t counters, size_t data_bytes, WsView &out) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    DeviceWorkspace &w = g_ws[dev];
-    if (w.ctr_cap < counters || w.data_bytes < data_bytes) {
-        size_t cc = w.ctr_cap > counters ? w.ctr_cap : counters;
-        if (cc < 4096) cc = 4096;
-        cc = (cc + 63) & ~(size_t)63;
-        size_t db = w.data_bytes > data_bytes ? w.data_bytes : data_bytes;
-        if (db < (1u << 20)) db = 1u << 20;
-        if (w.ptr) {
-            if (hipDeviceSynchronize() != hipSuccess) return false;
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.ctr_cap = w.data_bytes = 0;
-        }
-        if (hipMalloc(&w.ptr, cc * 4 + db) != hipSuccess) { w.ptr = nullptr; return false; }
-        if (hipMemset(w.ptr, 0, cc * 4 + db) != hipSuccess) return false;
-        w.ctr_cap = cc;
-        w.data_bytes = db;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    WsBuf *w = nullptr;
+    for (auto &e : g_ws)
+        if (e.dev == dev && e.stream == stream && e.kind == kind) { w = &e; break; }
+    if (!w) {
+        g_ws.push_back(WsBuf{dev, stream, kind, nullptr, 0, 0});
+        w = &g_ws.back();
     }
-    out.counters = (uint32_t *)w.ptr;
-    out.data = (unsigned char *)w.ptr + w.ctr_cap * 4;
+    if (w->ctr_cap < counters || w->data_bytes < data_bytes) {
+        size_t cc = w->ctr_cap > counters ? w->ctr_cap : counters;
+        if (kind == 0 && cc < 4096) cc = 4096;
+        cc = (cc + 63) & ~(size_t)63;
+        size_t db = w->data_bytes > data_bytes ? w->data_bytes : data_bytes;
+        if (db < (1u << 20)) db = 1u << 20;
+        if (w->ptr) {
+            /* the stream's earlier kernels may still use the old buffer */
+            if (hipStreamSynchronize(stream) != hipSuccess) return false;
+            (void)hipFree(w->ptr);
+            w->ptr = nullptr;
+            w->ctr_cap = w->data_bytes = 0;
+        }
+        if (hipMalloc(&w->ptr, cc * 4 + db) != hipSuccess) { w->ptr = nullptr; return false; }
+        if (cc > 0 && hipMemset(w->ptr, 0, cc * 4) != hipSuccess) return false;
+        w->ctr_cap = cc;
+        w->data_bytes = db;
+    }
+    out.counters = (uint32_t *)w->ptr;
+    out.data = (unsigned char *)w->ptr + w->ctr_cap * 4;
     return true;
 }
 
 size_t fixed_lds(const dlk::LdsPlan &pl) {
     return r16(32 * 8) + r16(64 * 8) + r16(16 * 8) + r16(64 * 4) + 4 * r16((size_t)pl.hcap * 4) +
            r16((size_t)pl.flag_words * 4);
+}
+
+/* The parameter block for rows r0.. of the batch: every per-row pointer moved on. */
+dlk::RowParams rows_from(const dlk::RowParams &p, int r0) {
+    dlk::RowParams q = p;
+    q.logits = p.logits + (int64_t)r0 * p.ld;
+    if (p.hist_off) q.hist_off = p.hist_off + r0;
+    if (p.mask) {
+        if (p.mask_row) q.mask_row = p.mask_row + r0;
+        else q.mask = p.mask + (int64_t)r0 * p.mask_ld;
+    }
+    if (p.rng) q.rng = p.rng + r0;
+    q.out_ids = p.out_ids + r0;
+    if (p.out_cand_ids) q.out_cand_ids = p.out_cand_ids + (int64_t)r0 * p.n_out;
+    if (p.out_cand_probs) q.out_cand_probs = p.out_cand_probs + (int64_t)r0 * p.n_out;
+    if (p.out_cand_logprobs) q.out_cand_logprobs = p.out_cand_logprobs + (int64_t)r0 * p.n_out;
+    return q;
 }
 
 /* Single-pass top-k path (sampler_topk.hip): returns DLK_OK, or 1 when the
@@ -135,7 +173,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
     size_t n_cand = (size_t)rows * G * KP * 8;
     WsView ws;
-    if (!workspace((size_t)rows, n_slot + n_cand, ws)) return DLK_ERR_HIP;
+    if (!workspace(stream, 0, (size_t)rows, n_slot + n_cand, ws)) return DLK_ERR_HIP;
     f.counters = ws.counters;
     f.slots = (TopkSlot *)ws.data;
     f.cands = (uint64_t *)(ws.data + n_slot);
@@ -147,7 +185,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
 int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStream_t stream) {
     using namespace dlk;
     const int T = kFullThreads;
-    if (p.greedy || p.topk_on || p.minp_on) return 1;
+    if (p.greedy || p.topk_on || p.minp_on || p.s_general) return 1;
     if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     if (vocab < 8192 || (vocab & 3) != 0) return 1;   /* whole 16-byte groups per row */
@@ -199,7 +237,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     WsView ws;
     /* the published words live in the zeroed counter region: they are zero
      * between launches (the kernel returns them to zero) */
-    if (!workspace((size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
+    if (!workspace(stream, 0, (size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
                    n_cv + n_wr + n_wv + 2 * n_wh + (size_t)rows_per * fb_bytes, ws))
         return DLK_ERR_HIP;
     f.sync = ws.counters;
@@ -213,33 +251,79 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     f.fb_bytes = fb_bytes;
     for (int r0 = 0; r0 < rows; r0 += rows_per) {
         const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;
-        f.p = p;
-        f.p.logits = p.logits + (int64_t)r0 * p.ld;
-        if (p.hist_off) f.p.hist_off = p.hist_off + r0;
-        if (p.mask) {
-            if (p.mask_row) f.p.mask_row = p.mask_row + r0;
-            else f.p.mask = p.mask + (int64_t)r0 * p.mask_ld;
-        }
-        f.p.rng = p.rng + r0;
-        f.p.out_ids = p.out_ids + r0;
-        if (p.out_cand_ids) f.p.out_cand_ids = p.out_cand_ids + (int64_t)r0 * p.n_out;
-        if (p.out_cand_probs) f.p.out_cand_probs = p.out_cand_probs + (int64_t)r0 * p.n_out;
-        if (p.out_cand_logprobs) f.p.out_cand_logprobs = p.out_cand_logprobs + (int64_t)r0 * p.n_out;
+        f.p = rows_from(p, r0);
         if (dlk_launch_full_kernel(&f, nr, ept, lds, stream) != 0) return DLK_ERR_HIP;
     }
     return DLK_OK;
 }
 
-}  // namespace
+/* The row kernel with a top-k too large for LDS: candidates (two buffers for
+ * the sort) and the pipeline's aggregates in workspace, rows in chunks. */
+int launch_row_global_topk(dlk::RowParams &p, int rows, hipStream_t stream) {
+    const int64_t kpad = ((int64_t)p.top_k + 63) & ~(int64_t)63;
+    const size_t cand_bytes = (size_t)kpad * 2 * 8;
+    const size_t reg_bytes = r16(aggs_bytes(p.top_k));
+    const size_t per_row = cand_bytes + reg_bytes;
+    int rows_per = (int)(kGlobalTopkBudget / per_row);
+    if (rows_per < 1) rows_per = 1;
+    if (rows_per > rows) rows_per = rows;
+    WsView ws;
+    if (!workspace(stream, 0, 0, (size_t)rows_per * per_row, ws)) return DLK_ERR_HIP;
+    p.gcand = (uint64_t *)ws.data;
+    p.gcand_stride = kpad * 2;
+    p.gregion = ws.data + (size_t)rows_per * cand_bytes;
+    p.gregion_stride = (int64_t)reg_bytes;
+    const size_t total = fixed_lds(p.plan) + r16(2048 * 4) + r16((size_t)kLsdWords * 4);
+    if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;
+    p.plan.bytes = (int)total;
+    for (int r0 = 0; r0 < rows; r0 += rows_per) {
+        const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;
+        dlk::RowParams q = rows_from(p, r0);
+        if (dlk_launch_row_kernel(&q, nr, total, stream) != 0) return DLK_ERR_HIP;
+    }
+    return DLK_OK;
+}
 
-extern "C" uint64_t dlk_seed_state(uint64_t seed) { return seed ? seed : 0xDEADBEEF12345678ULL; }
-
-extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sample_params *prm,
-                          hipStream_t stream) {
+int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params *prm, hipStream_t stream) {
     if (!b || !prm || rows <= 0 || vocab <= 0 || !b->logits || !b->out_ids || b->ld < vocab) return DLK_ERR_INVALID;
     if (prm->n_out < 0) return DLK_ERR_INVALID;
     if ((b->hist_off == nullptr) != (b->hist_ids == nullptr)) return DLK_ERR_INVALID;
     if (b->mask && b->mask_ld < (vocab + 31) / 32) return DLK_ERR_INVALID;
+    const bool greedy = prm->temperature == 0.0f;               /* src/sampler.c:140 */
+    if (!greedy && !b->rng) return DLK_ERR_INVALID;
+    const int max_hist = prm->max_history > 0 ? prm->max_history : 1024;
+    const bool cap_on = prm->softcap > 0.0f;                    /* src/core/context.c:604 */
+    if (cap_on || (b->hist_off && pow2_at_least(max_hist, 64) > kHcapDirect)) {
+        /* the rows as sampler_sample would see them -- soft-cap, mask, penalties
+         * (src/core/sampler_api.c:51-61) -- in a scratch copy; then the sampling
+         * alone over the copy */
+        if (rows > 65535) return DLK_ERR_UNSUPPORTED;
+        const int64_t ldp = ((int64_t)vocab + 63) & ~(int64_t)63;
+        WsView ws;
+        if (!workspace(stream, 1, 0, (size_t)rows * ldp * 4, ws)) return DLK_ERR_HIP;
+        float *prep = (float *)ws.data;
+        if (dlk_launch_prepare_rows(b->logits, b->ld, prep, ldp, rows, vocab, b->mask, b->mask_ld, b->mask_row,
+                                    cap_on ? prm->softcap : 0.0f, stream) != 0)
+            return DLK_ERR_HIP;
+        if (b->hist_off) {
+            const int rc = dlk_apply_penalties(prep, ldp, rows, vocab, b->hist_off, b->hist_ids, prm->penalty_order,
+                                               prm->repeat_penalty, prm->frequency_penalty, prm->presence_penalty,
+                                               stream);
+            if (rc != DLK_OK) return rc;
+        }
+        dlk_batch b2 = *b;
+        b2.logits = prep;
+        b2.ld = ldp;
+        b2.hist_off = b2.hist_ids = nullptr;
+        b2.mask = nullptr;
+        b2.mask_row = nullptr;
+        b2.mask_ld = 0;
+        dlk_sample_params p2 = *prm;
+        p2.softcap = 0.0f;
+        p2.max_history = 0;
+        return sample_impl(&b2, rows, vocab, &p2, stream);
+    }
+
     dlk::RowParams p;
     memset(&p, 0, sizeof(p));
     p.logits = b->logits; p.ld = b->ld; p.V = vocab;
@@ -251,25 +335,26 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
     p.top_p = prm->top_p; p.min_p = prm->min_p;
     p.rep = prm->repeat_penalty; p.freq = prm->frequency_penalty; p.pres = prm->presence_penalty;
     p.order = prm->penalty_order;
-    p.greedy = prm->temperature == 0.0f;                        /* src/sampler.c:140 */
+    p.greedy = greedy;
     if (!p.greedy) {
-        if (!b->rng) return DLK_ERR_INVALID;
         p.inv_temp = 1.0f / prm->temperature;                   /* src/sampler.c:154 */
-        if (!(p.inv_temp > 0.0f) || isinf(p.inv_temp)) return DLK_ERR_UNSUPPORTED;
+        /* 1/T negative, zero or infinite: s = (l - max) * (1/T) may be NaN or +inf
+         * and its maximum is not 0; the row kernel handles it */
+        p.s_general = !(p.inv_temp > 0.0f && p.inv_temp < INFINITY);
     }
     p.topk_on = prm->top_k > 0 && prm->top_k < vocab;           /* src/sampler.c:166 */
     p.top_k = prm->top_k;
-    if (p.topk_on && prm->top_k > kMaxTopK) return DLK_ERR_UNSUPPORTED;
     p.topp_on = prm->top_p < 1.0f;                              /* src/sampler.c:205 */
     p.topp_thr = (p.topp_on && prm->top_p > 0.0f) ? topp_threshold(prm->top_p) : 0.0;
     p.minp_on = prm->min_p > 0.0f;                              /* src/sampler.c:188 */
 
     dlk::LdsPlan &pl = p.plan;
-    int max_hist = prm->max_history > 0 ? prm->max_history : 1024;
     pl.hcap = b->hist_off ? pow2_at_least(max_hist, 64) : 64;
     int nch = (vocab + 63) / 64;
     pl.flag_words = (nch + 31) / 32;
-    pl.kp = p.topk_on ? pow2_at_least(p.top_k, 64) : 0;
+    const bool big_k = p.topk_on && !p.greedy && p.top_k > kMaxTopKLds;
+    pl.kp = p.topk_on && !big_k ? pow2_at_least(p.top_k, 64) : 0;
+    if (big_k) return launch_row_global_topk(p, rows, stream);
     size_t fixed = fixed_lds(pl);
     size_t region = 0;
     if (!p.greedy) {
@@ -277,7 +362,7 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
         else region = aggs_bytes(vocab);
     }
     size_t total = fixed + region;
-    if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on)) {
+    if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on) && !p.s_general) {
         int rc = launch_topk(p, rows, vocab, stream);
         if (rc <= 0) return rc;
     }
@@ -288,4 +373,31 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
     if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;
     pl.bytes = (int)total;
     return dlk_launch_row_kernel(&p, rows, total, stream) == 0 ? DLK_OK : DLK_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" uint64_t dlk_seed_state(uint64_t seed) { return seed ? seed : 0xDEADBEEF12345678ULL; }
+
+extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sample_params *prm,
+                          hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    return sample_impl(b, rows, vocab, prm, stream);
+}
+
+/* Frees the workspace buffers of `stream` on the current device (the drop-ins
+ * call it before they destroy a stream).  Not exported. */
+extern "C" void dlk_internal_release_stream(hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    for (size_t i = 0; i < g_ws.size();) {
+        if (g_ws[i].dev == dev && g_ws[i].stream == stream) {
+            (void)hipStreamSynchronize(stream);
+            (void)hipFree(g_ws[i].ptr);
+            g_ws.erase(g_ws.begin() + (long)i);
+        } else {
+            i++;
+        }
+    }
 }

@@ -12,7 +12,7 @@
 namespace dlk {
 
 constexpr int kPenThreads = 256;
-constexpr int kPenLds = 4096;          /* history entries staged in LDS; longer ones are read from memory */
+constexpr int kPenLds = 16384;         /* history entries staged in LDS; longer ones are read from memory */
 
 __device__ __forceinline__ float penalize_ops(float x, int cnt, uint32_t order, float rep, float freq, float pres) {
     for (int s = 0; s < 8; s++) {

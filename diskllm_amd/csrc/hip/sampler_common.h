@@ -322,10 +322,14 @@ __device__ __forceinline__ int build_patches(const RowParams &p, int row, const 
 
 /* ------------------------------------------------------------- exact top-k */
 
-/* First k elements under (s desc, index asc), sorted, into cand[0..k) as
- * (desc_key << 32 | index).  Radix select on the 32-bit key (11/11/10 bits),
- * then collection; ties at the k-th key are taken in index order. */
-__device__ __forceinline__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32_t *hist, Lds &L) {
+/* The key of the k-th element (1-based) under (s desc, index asc), as
+ * desc_key(s): radix select on the 32-bit key (11/11/10 bits).  Also returns
+ * how many keys are below it and how many equal it. */
+struct KthKey {
+    uint32_t key;
+    int below, equal;
+};
+__device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist, Lds &L) {
     const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id();
     uint32_t prefix = 0;
     int krem = k, below_total = 0, eq_count = 0;
@@ -376,7 +380,17 @@ __device__ __forceinline__ void select_top_k(const Row &R, int k, uint64_t *cand
         krem -= below;
         below_total += below;
     }
-    const uint32_t kstar = prefix;
+    return KthKey{prefix, below_total, eq_count};
+}
+
+/* First k elements under (s desc, index asc), sorted, into cand[0..k) as
+ * (desc_key << 32 | index): the k-th key by radix select, then collection;
+ * ties at the k-th key are taken in index order. */
+__device__ __forceinline__ void select_top_k(const Row &R, int k, uint64_t *cand, int kp, uint32_t *hist, Lds &L) {
+    const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id();
+    const KthKey kk = radix_kth(R, k, hist, L);
+    const int below_total = kk.below, eq_count = kk.equal;
+    const uint32_t kstar = kk.key;
     const int need = k - below_total;     /* >= 1 elements with key == kstar */
     int *cnt = L.bi + 8;                  /* [0] appended, [1] ties taken */
     if (t == 0) { cnt[0] = 0; cnt[1] = 0; }
@@ -418,6 +432,110 @@ __device__ __forceinline__ void select_top_k(const Row &R, int k, uint64_t *cand
     for (int i = k + t; i < kp; i += T) cand[i] = ~0ull;
     __syncthreads();
     bitonic_sort(cand, kp);
+}
+
+/* Inclusive block prefix of per-thread u32 values in thread order; `total` is
+ * the block's sum (red: one word per wave). */
+DLK_DEV uint32_t block_incl_prefix_u32t(uint32_t v, uint32_t *red, uint32_t &total) {
+    const int lane = lane_id(), w = wave_id(), nw = n_waves();
+    const uint32_t inc = wave_scan_sat_u32(v, 0xffffffffu);
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    const uint32_t wt = wave_scan_sat_u32(lane < nw ? red[lane] : 0u, 0xffffffffu);
+    const uint32_t base = w > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)wt, w - 1) : 0u;
+    total = (uint32_t)__builtin_amdgcn_readlane((int)wt, nw - 1);
+    __syncthreads();
+    return base + inc;
+}
+
+/* LDS words select_top_k_global needs (bucket bases and per-wave digit counts). */
+constexpr int kLsdWords = 256 + 16 * 256 + 16;
+
+/* select_top_k for a k too large for LDS: the first k elements under (s desc,
+ * index asc), sorted, into a[0..k) (global memory; b[0..k) is the sort's second
+ * buffer).  The k-th key by radix select; the candidates collected in index
+ * order (ties at the k-th key: the first ones in index order, as the
+ * reference's insertion sort keeps them, src/sampler.c:122,127); then a stable
+ * LSD radix sort on the 32-bit s key, 4 passes of 8 bits, which keeps equal keys
+ * in index order.  Needs blockDim.x <= 1024. */
+__device__ __forceinline__ void select_top_k_global(const Row &R, int k, uint64_t *a, uint64_t *b, uint32_t *hist,
+                                                    uint32_t *lsd, Lds &L) {
+    const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id(), w = wave_id(), nw = n_waves();
+    const KthKey kk = radix_kth(R, k, hist, L);
+    const int need = k - kk.below;                 /* ties at the k-th key to take, >= 1 */
+    uint32_t *red = lsd + 256 + 16 * 256;
+    /* ---- collection in index order: a tile of T elements at a time -------- */
+    int base_lt = 0, base_tie = 0;
+    for (int i0 = 0; i0 < V; i0 += T) {
+        const int i = i0 + t;
+        const uint32_t key = i < V ? desc_key(scaled(R, i)) : 0xffffffffu;
+        const bool lt = i < V && key < kk.key, tie = i < V && key == kk.key;
+        const uint32_t v = (lt ? 1u : 0u) | (tie ? 0x10000u : 0u);
+        uint32_t tot = 0;
+        const uint32_t ex = block_incl_prefix_u32t(v, red, tot) - v;
+        const int lt_before = base_lt + (int)(ex & 0xffffu), tie_before = base_tie + (int)(ex >> 16);
+        if (lt || (tie && tie_before < need))
+            a[lt_before + min(tie_before, need)] = ((uint64_t)key << 32) | (uint32_t)i;
+        base_lt += (int)(tot & 0xffffu);
+        base_tie += (int)(tot >> 16);
+    }
+    __syncthreads();
+    /* ---- stable LSD radix sort of a[0..k) on bits 32..63 ------------------- */
+    uint32_t *cnt = lsd, *wc = lsd + 256;
+    uint64_t *src = a, *dst = b;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    for (int pass = 0; pass < 4; pass++) {
+        const int sh = 32 + 8 * pass;
+        for (int d = t; d < 256; d += T) cnt[d] = 0;
+        __syncthreads();
+        for (int i = t; i < k; i += T) atomicAdd(&cnt[(uint32_t)(src[i] >> sh) & 255u], 1u);
+        __syncthreads();
+        if (w == 0) {
+            const uint32_t c0 = cnt[4 * lane], c1 = cnt[4 * lane + 1], c2 = cnt[4 * lane + 2], c3 = cnt[4 * lane + 3];
+            const uint32_t s4 = c0 + c1 + c2 + c3;
+            const uint32_t ex = wave_scan_sat_u32(s4, 0xffffffffu) - s4;
+            cnt[4 * lane] = ex;
+            cnt[4 * lane + 1] = ex + c0;
+            cnt[4 * lane + 2] = ex + c0 + c1;
+            cnt[4 * lane + 3] = ex + c0 + c1 + c2;
+        }
+        __syncthreads();
+        for (int i0 = 0; i0 < k; i0 += T) {
+            const int i = i0 + t;
+            const bool valid = i < k;
+            const uint64_t e = valid ? src[i] : 0ull;
+            const uint32_t d = (uint32_t)(e >> sh) & 255u;
+            for (int j = t; j < 16 * 256; j += T) wc[j] = 0;
+            /* lanes of this wave holding the same digit (8 ballots) */
+            uint64_t m = ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 8; bit++) {
+                const uint64_t bb = ballot(valid && ((d >> bit) & 1u));
+                m &= ((d >> bit) & 1u) ? bb : ~bb;
+            }
+            const int rank = __popcll(m & lt_mask);
+            __syncthreads();
+            if (valid && rank == 0) wc[w * 256 + d] = (uint32_t)__popcll(m);
+            __syncthreads();
+            /* per digit: the waves' offsets in order, then the bucket moves on */
+            for (int dd = t; dd < 256; dd += T) {
+                uint32_t acc = cnt[dd];
+                for (int ww = 0; ww < nw; ww++) {
+                    const uint32_t c = wc[ww * 256 + dd];
+                    wc[ww * 256 + dd] = acc;
+                    acc += c;
+                }
+                cnt[dd] = acc;
+            }
+            __syncthreads();
+            if (valid) dst[wc[w * 256 + d] + (uint32_t)rank] = e;
+            __syncthreads();
+        }
+        uint64_t *tmp = src;
+        src = dst;
+        dst = tmp;
+    }
+    /* four passes: the sorted keys are back in a */
 }
 
 /* -------------------------------------------------------- sampling pipeline */
@@ -501,6 +619,10 @@ __device__ __forceinline__ ResolveOut<MB> exact_sum(int n, const QF &q, const Ag
 /* The reference's softmax/min-p/top-p/draw over n candidate positions.
  * Returns the sampled position; fills S. */
 /* ------------------------------------------------- rows holding NaN or +inf */
+
+/* Largest k for which a row whose s holds NaN runs emulate_topk_row (the
+ * reference's O(V k) insertion sort on one thread). */
+constexpr int kEmulateMaxK = 4096;
 
 /* Top-k rows holding NaN or +inf after the mask and penalties: once NaN takes
  * part, the reference's insertion sort keeps NaN entries in place and stops

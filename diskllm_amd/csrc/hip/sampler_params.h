@@ -40,6 +40,15 @@ struct RowParams {
     uint32_t order;
     double topp_thr;     /* smallest double d with (float)d >= top_p */
     int greedy, topk_on, topp_on, minp_on;
+    /* 1/temperature outside (0, inf): s = (l - max) * (1/T) may hold NaN or +inf
+     * and its maximum is not 0 (row kernel only) */
+    int s_general;
+    /* top-k too large for LDS (row kernel only): per row, 2 * gcand_stride/2
+     * candidate entries (sort ping-pong) and the pipeline's aggregates */
+    uint64_t *gcand;
+    int64_t gcand_stride;
+    unsigned char *gregion;
+    int64_t gregion_stride;
     LdsPlan plan;
 };
 

@@ -68,16 +68,58 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
     if (t == 0) p.rng[row] = st;
 
     const int k = p.topk_on ? p.top_k : V;
-    if (irr && p.topk_on) {
-        if (t == 0) emulate_topk_row(p, R, k, r, (uint64_t *)L.region, row);
+    /* s = (l - max) * (1/T) holding NaN (snan) or +inf (spinf): with 1/T in
+     * (0, inf) exactly when a prepared logit is NaN or +inf; otherwise checked
+     * on s itself, whose maximum (src/sampler.c:173-176) is then not 0 */
+    bool snan = irr != 0, spinf = false;
+    float maxs = 0.0f;
+    R.M = bv;
+    if (p.s_general && !irr && bv > -INFINITY) {
+        float m = -INFINITY;
+        int fl = 0;
+        for (int i = t; i < V; i += blockDim.x) {
+            const float s = scaled(R, i);
+            if (s != s) fl |= 1;
+            else if (s == INFINITY) fl |= 2;
+            else m = fmaxf(m, s);
+        }
+        m = wave_max_dpp(m);
+        for (int o = 32; o >= 1; o >>= 1) fl |= shfl_xor(fl, o);
+        float *rm = (float *)L.red;
+        int *rf = (int *)(L.red + 32);
+        if (lane == 0) { rm[wave_id()] = m; rf[wave_id()] = fl; }
+        __syncthreads();
+        m = -INFINITY;
+        fl = 0;
+        for (int w2 = 0; w2 < n_waves(); w2++) { m = fmaxf(m, rm[w2]); fl |= rf[w2]; }
+        __syncthreads();
+        snan = (fl & 1) != 0;
+        spinf = (fl & 2) != 0;
+        maxs = m;
+    }
+    if (snan && p.topk_on && (k <= kEmulateMaxK || bv > -INFINITY)) {
+        if (k <= kEmulateMaxK) {
+            if (t == 0) emulate_topk_row(p, R, k, r, (uint64_t *)L.region, row);
+        } else {
+            /* the reference's insertion sort with NaN keys, O(V k) on one thread,
+             * is not run for large k */
+            if (t == 0) {
+                p.out_ids[row] = -1;
+                if (p.status) atomicOr(p.status, DLK_STATUS_UNSUPPORTED_ROW);
+            }
+            for (int j = t; j < n_out; j += blockDim.x) {
+                if (p.out_cand_ids) p.out_cand_ids[(int64_t)row * n_out + j] = -1;
+                if (p.out_cand_probs) p.out_cand_probs[(int64_t)row * n_out + j] = NAN;
+                if (p.out_cand_logprobs) p.out_cand_logprobs[(int64_t)row * n_out + j] = NAN;
+            }
+        }
         return;
     }
-    if (irr || !(bv > -INFINITY)) {
-        /* without top-k a NaN or +inf entry makes the softmax sum NaN (+inf - max
-         * is NaN): as for a row of -inf, no comparison with it holds and the draw
-         * falls through to the last candidate */
-        /* every entry -inf: the softmax is NaN throughout and the draw falls
-         * through to the last candidate, which is index k-1 in index order */
+    if (((snan || spinf) && !p.topk_on) || !(bv > -INFINITY)) {
+        /* without top-k a NaN or +inf entry of s makes the softmax sum NaN (+inf -
+         * max is NaN): as for a row of -inf, no comparison with it holds and the
+         * draw falls through to the last candidate, which is index k-1 in index
+         * order (every s of a row of -inf is NaN, so the top-k sort moves nothing) */
         if (t == 0) p.out_ids[row] = k - 1;
         for (int j = t; j < n_out; j += blockDim.x) {
             if (p.out_cand_ids) p.out_cand_ids[(int64_t)row * n_out + j] = j < k ? j : -1;
@@ -86,17 +128,39 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
         }
         return;
     }
-    R.M = bv;
     Scal S;
     int pos, tok;
     if (p.topk_on) {
-        const int kp = pl.kp;
-        uint64_t *cand = (uint64_t *)L.region;
-        uint32_t *hist = (uint32_t *)(L.region + (size_t)kp * 8);
-        select_top_k(R, k, cand, kp, hist, L);
+        uint64_t *cand;
+        unsigned char *reg;
+        if (p.gcand) {
+            /* k too large for LDS: candidates and aggregates in global memory */
+            cand = p.gcand + (int64_t)row * p.gcand_stride;
+            reg = p.gregion + (int64_t)row * p.gregion_stride;
+            uint32_t *hist = (uint32_t *)L.region;
+            select_top_k_global(R, k, cand, cand + p.gcand_stride / 2, hist, hist + 2048, L);
+        } else {
+            const int kp = pl.kp;
+            cand = (uint64_t *)L.region;
+            uint32_t *hist = (uint32_t *)(L.region + (size_t)kp * 8);
+            select_top_k(R, k, cand, kp, hist, L);
+            reg = L.region + (size_t)kp * 8;
+        }
         CandBase cb{&R, cand};
         R.maxv = cb.s(0);                 /* sorted: buf[0] is the maximum (src/sampler.c:173-176) */
-        unsigned char *reg = L.region + (size_t)kp * 8;
+        if (spinf) {
+            /* +inf at the top of the sorted candidates, no NaN: e is NaN there and 0
+             * elsewhere, so the sum, every probability and every comparison of the
+             * draw are NaN and the draw falls through to buf[k-1] (src/sampler.c:233) */
+            if (t == 0) p.out_ids[row] = cb.token(k - 1);
+            for (int j = t; j < n_out; j += blockDim.x) {
+                int64_t o = (int64_t)row * n_out + j;
+                if (p.out_cand_ids) p.out_cand_ids[o] = j < k ? cb.token(j) : -1;
+                if (p.out_cand_probs) p.out_cand_probs[o] = j < k ? NAN : 0.0f;
+                if (p.out_cand_logprobs) p.out_cand_logprobs[o] = -INFINITY;
+            }
+            return;
+        }
         pos = pipeline(p, cb, k, r, reg, L, S);
         tok = cb.token(pos);
         if (t == 0) p.out_ids[row] = tok;
@@ -116,6 +180,7 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
             }
         }
     } else {
+        R.maxv = maxs;                    /* 0 unless 1/T is outside (0, inf) */
         FullBase fb{&R};
         pos = pipeline(p, fb, V, r, L.region, L, S);
         if (t == 0) p.out_ids[row] = pos;

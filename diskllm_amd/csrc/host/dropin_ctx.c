@@ -19,8 +19,13 @@ fail:
     return -1;
 }
 
+void dlk_internal_release_stream(hipStream_t stream);   /* capi.hip: the stream's workspace */
+
 void dlk_dropin_release(dlk_dropin_ctx *c) {
-    if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->stream) {
+        hipStreamSynchronize(c->stream);
+        dlk_internal_release_stream(c->stream);
+    }
     hipFree(c->logits);
     hipFree(c->hist);
     hipFree(c->hoff);

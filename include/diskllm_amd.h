@@ -34,6 +34,7 @@ extern "C" {
 /* Device status bits written by the kernels (dlk_batch.status). */
 #define DLK_STATUS_HISTORY_TOO_LONG 1u  /* a row's history exceeded max_history: its id is -1 */
 #define DLK_STATUS_SYNC_TIMEOUT 2u      /* a cross-workgroup wait gave up (results of the call invalid) */
+#define DLK_STATUS_UNSUPPORTED_ROW 4u   /* a row whose s = (l - max) / T holds NaN with top_k > 4096: its id is -1 */
 
 /* Penalty ops, packed low nibble first into dlk_sample_params.penalty_order. */
 #define DLK_OP_REPETITION 1u  /* src/sampler.c:21-33, once per occurrence */
@@ -46,8 +47,9 @@ extern "C" {
 
 typedef struct {
     /* sampler_config (include/sampler.h:10-16) without the seed: */
-    float temperature;        /* 0 = greedy; otherwise 1/temperature must be finite and > 0 */
-    int top_k;                /* active when 0 < top_k < vocab; at most 4096 */
+    float temperature;        /* 0 = greedy; any other value as the reference uses it (1/temperature
+                                 negative, zero or infinite included, src/sampler.c:154) */
+    int top_k;                /* active when 0 < top_k < vocab */
     float top_p;              /* active when < 1 */
     float min_p;              /* active when > 0 (absolute threshold, src/sampler.c:189) */
     /* penalties (diskllm_sampler_params, include/diskllm.h:48-56, plus frequency): */
@@ -55,9 +57,12 @@ typedef struct {
     float frequency_penalty;  /* active when != 0 */
     float presence_penalty;   /* active when != 0 */
     uint32_t penalty_order;   /* DLK_ORDER_* or any packing of DLK_OP_* */
-    int max_history;          /* upper bound on any row's history length (LDS sizing) */
+    int max_history;          /* upper bound on any row's history length (0 = 1024); above 1024 the
+                                 penalties are applied to a scratch copy of the rows first */
     int n_out;                /* candidate outputs per row (0 = none) */
     int path;                 /* DLK_PATH_AUTO; the others force one implementation (tests) */
+    float softcap;            /* > 0: logits = softcap * tanhf(logits / softcap) first, as the
+                                 reference's decode step does (src/core/context.c:873-876); else none */
 } dlk_sample_params;
 
 #define DLK_PATH_AUTO 0        /* fastest path that covers the configuration */

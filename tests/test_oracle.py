@@ -227,6 +227,41 @@ def test_sample_vs_reference(V, T, k, p, mp, seed):
             np.testing.assert_array_equal(o["final"][:n].view(np.uint32), rv.view(np.uint32))
 
 
+def _boundary_configs():
+    """1/temperature negative, zero and infinite (src/sampler.c:154 uses it as
+    is), and top-k far past LDS sizes (any 0 < top_k < V, :166)."""
+    out = []
+    for V in (7, 1000, 20000):
+        for (T, k, p, mp) in ((-0.5, 0, 0.9, 0.0), (-2.0, 40, 0.95, 0.0), (-1.0, 0, 1.0, 0.05),
+                              (1e-40, 0, 0.9, 0.0), (1e-40, 5, 1.0, 0.0), (float("inf"), 0, 0.9, 0.0),
+                              (float("inf"), 3, 1.0, 0.0), (1.0, V // 2, 0.9, 0.0), (0.7, V - 1, 0.95, 0.0),
+                              (-0.7, V - 1, 0.8, 0.0), (1.2, max(1, V - 5), 1.0, 0.01)):
+            if 0 < k < V or k == 0:
+                out.append((V, T, k, p, mp))
+    return out
+
+
+@needs_ref
+@pytest.mark.parametrize("V,T,k,p,mp", _boundary_configs())
+def test_sample_vs_reference_boundary(V, T, k, p, mp):
+    """The oracle's token and rng state equal the strict reference build's on the
+    configurations outside the usual range, over rows with ties, masked (-inf)
+    entries (+inf under a negative temperature) and large spreads."""
+    rng = np.random.default_rng(V * 7 + k)
+    for rep in range(4):
+        row = rng.normal(0, 3, V).astype(np.float32)
+        if rep == 1:
+            row = np.round(row)
+        if rep == 2 and V > 3:
+            row[rng.random(V) < 0.2] = -np.inf
+        if rep == 3:
+            row[: V // 2] *= 1e37                                      # (l - max) overflows to -inf
+        st = int(rng.integers(1, 2 ** 63))
+        tok, st_ref, _, _ = O.ref_sample_row("strict", row, st, T, k, p, mp, n_trace=1)
+        o = O.sample_row(row, st, T, k, p, mp)
+        assert o["token"] == tok and o["state"] == st_ref, (rep, o["token"], tok)
+
+
 @needs_ref
 def test_fast_build_agreement():
     """Agreement of the reference's Makefile build (-O3 -ffast-math, libmvec expf)
