@@ -70,7 +70,7 @@ class GrammarRow(C.Structure):
 # Every symbol the public headers declare (checked by the CPU test suite).
 EXPORTS = [
     # include/diskllm_amd.h
-    "dlk_seed_state", "dlk_sample", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
+    "dlk_seed_state", "dlk_sample", "dlk_sample_noalloc", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
     "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
     "dlk_vocab_csr_from_gguf", "dlk_softcap",
     # include/sampler.h
@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
         L.dlk_seed_state.argtypes = [C.c_uint64]
         L.dlk_sample.restype = C.c_int
         L.dlk_sample.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p]
+        L.dlk_sample_noalloc.restype = C.c_int
+        L.dlk_sample_noalloc.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p]
         L.dlk_dfa_mask.restype = C.c_int
         L.dlk_dfa_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                    C.c_int, C.c_uint64, C.c_void_p, C.c_int64, C.c_void_p]

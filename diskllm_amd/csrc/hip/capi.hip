@@ -78,7 +78,59 @@ struct WsView {
     unsigned char *data;
 };
 
+/* ---- the no-allocation entry point's scratch ----------------------------------
+ * dlk_sample_noalloc takes its workspace from this fixed array instead: every
+ * device the library runs on holds one copy of it until the process ends.  The
+ * first kScratchCtrWords words are the counter region, the rest is scratch.  In
+ * host code `scratch` names a host-side stand-in, never the device memory: the
+ * device address comes from hipGetSymbolAddress, once per device, with that
+ * device current (scratch_ptr), and only that address is handed to kernels. */
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr size_t kScratchCtrWords = (size_t)1 << 16;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+unsigned char *g_scratch_dev[64];     /* per device: the address of its copy */
+bool g_noalloc = false;               /* set (under g_mu) for a dlk_sample_noalloc call */
+int g_ws_err = DLK_ERR_HIP;           /* why the last workspace() failed */
+
+__global__ void zero_words_kernel(uint32_t *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+unsigned char *scratch_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!g_scratch_dev[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_dev[dev] = (unsigned char *)ptr;
+    }
+    return g_scratch_dev[dev];
+}
+
+/* The no-allocation workspace: the scratch array, its counter words this call
+ * uses cleared by a fill kernel on the call's stream (a kernel, not a memset
+ * node, so that the call may be captured into a graph). */
+bool workspace_noalloc(hipStream_t stream, int kind, size_t counters, size_t data_bytes, WsView &out) {
+    g_ws_err = DLK_ERR_UNSUPPORTED;
+    if (kind != 0 || counters > kScratchCtrWords || data_bytes > kScratchBytes - kScratchCtrWords * 4) return false;
+    unsigned char *base = scratch_ptr();
+    g_ws_err = DLK_ERR_HIP;
+    if (!base) return false;
+    if (counters > 0) {
+        unsigned blocks = (unsigned)((counters + 255) / 256);
+        if (blocks > 1024) blocks = 1024;
+        hipLaunchKernelGGL(zero_words_kernel, dim3(blocks), dim3(256), 0, stream, (uint32_t *)base, counters);
+        if (hipGetLastError() != hipSuccess) return false;
+    }
+    out.counters = (uint32_t *)base;
+    out.data = base + kScratchCtrWords * 4;
+    return true;
+}
+
 bool workspace(hipStream_t stream, int kind, size_t counters, size_t data_bytes, WsView &out) {
+    if (g_noalloc) return workspace_noalloc(stream, kind, counters, data_bytes, out);
+    g_ws_err = DLK_ERR_HIP;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     WsBuf *w = nullptr;
@@ -173,7 +225,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
     size_t n_cand = (size_t)rows * G * KP * 8;
     WsView ws;
-    if (!workspace(stream, 0, (size_t)rows, n_slot + n_cand, ws)) return DLK_ERR_HIP;
+    if (!workspace(stream, 0, (size_t)rows, n_slot + n_cand, ws)) return g_ws_err;
     f.counters = ws.counters;
     f.slots = (TopkSlot *)ws.data;
     f.cands = (uint64_t *)(ws.data + n_slot);
@@ -239,7 +291,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
      * between launches (the kernel returns them to zero) */
     if (!workspace(stream, 0, (size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
                    n_cv + n_wr + n_wv + 2 * n_wh + (size_t)rows_per * fb_bytes, ws))
-        return DLK_ERR_HIP;
+        return g_ws_err;
     f.sync = ws.counters;
     f.pub = (uint64_t *)(ws.counters + (size_t)rows_per * kSyncWords);
     f.cvals = (float *)ws.data;
@@ -264,11 +316,12 @@ int launch_row_global_topk(dlk::RowParams &p, int rows, hipStream_t stream) {
     const size_t cand_bytes = (size_t)kpad * 2 * 8;
     const size_t reg_bytes = r16(aggs_bytes(p.top_k));
     const size_t per_row = cand_bytes + reg_bytes;
-    int rows_per = (int)(kGlobalTopkBudget / per_row);
+    const size_t budget = g_noalloc ? kScratchBytes - kScratchCtrWords * 4 : kGlobalTopkBudget;
+    int rows_per = (int)(budget / per_row);
     if (rows_per < 1) rows_per = 1;
     if (rows_per > rows) rows_per = rows;
     WsView ws;
-    if (!workspace(stream, 0, 0, (size_t)rows_per * per_row, ws)) return DLK_ERR_HIP;
+    if (!workspace(stream, 0, 0, (size_t)rows_per * per_row, ws)) return g_ws_err;
     p.gcand = (uint64_t *)ws.data;
     p.gcand_stride = kpad * 2;
     p.gregion = ws.data + (size_t)rows_per * cand_bytes;
@@ -300,7 +353,7 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
         if (rows > 65535) return DLK_ERR_UNSUPPORTED;
         const int64_t ldp = ((int64_t)vocab + 63) & ~(int64_t)63;
         WsView ws;
-        if (!workspace(stream, 1, 0, (size_t)rows * ldp * 4, ws)) return DLK_ERR_HIP;
+        if (!workspace(stream, 1, 0, (size_t)rows * ldp * 4, ws)) return g_ws_err;
         float *prep = (float *)ws.data;
         if (dlk_launch_prepare_rows(b->logits, b->ld, prep, ldp, rows, vocab, b->mask, b->mask_ld, b->mask_row,
                                     cap_on ? prm->softcap : 0.0f, stream) != 0)
@@ -400,4 +453,16 @@ extern "C" void dlk_internal_release_stream(hipStream_t stream) {
             i++;
         }
     }
+}
+
+/* dlk_sample with its workspace in the fixed per-device scratch array: no
+ * allocation of any kind.  The scratch is shared by every call on the device,
+ * so calls that overlap on one device race. */
+extern "C" int dlk_sample_noalloc(const dlk_batch *b, int rows, int vocab, const dlk_sample_params *prm,
+                                  hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_noalloc = true;
+    const int rc = sample_impl(b, rows, vocab, prm, stream);
+    g_noalloc = false;
+    return rc;
 }

@@ -94,6 +94,19 @@ uint64_t dlk_seed_state(uint64_t seed);
 int dlk_sample(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
                hipStream_t stream);
 
+/* dlk_sample without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and results as dlk_sample; its workspace is a fixed 32 MiB scratch array per
+ * device (held until the process ends), whose counter words each call clears
+ * with a fill kernel on `stream`.  Every call on a device shares that device's
+ * array, so calls that overlap on one device race.  DLK_ERR_UNSUPPORTED when the
+ * call needs more than the array holds or a second buffer: softcap > 0,
+ * max_history > 1024, or a batch whose kernels' workspace exceeds the array. */
+#define DLK_NOALLOC_SCRATCH_BYTES (32u << 20)
+int dlk_sample_noalloc(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
+                       hipStream_t stream);
+
 /* Byte-DFA allow-masks (no reference counterpart; replaces the accept_str
  * callback loop of src/core/grammar.c:284-306 for byte-level automata).
  * Token t = bytes[off[t] .. off[t+1]) is allowed from state s iff s != 0, the
