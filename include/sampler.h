@@ -5,9 +5,11 @@
  * device, runs the batched kernels of diskllm_amd.h on one row and copies the
  * result back.  Results are bit-identical to the reference built as strict ISO C.
  *
- * Each sampler owns a HIP stream and device buffers; like the reference's it is
- * not thread-safe.  greedy_sample and the two penalty functions take no sampler
- * and share one lazily created per-process context guarded by a mutex.
+ * Each sampler owns a HIP stream and device buffers (its own kernel workspace
+ * too), so separate samplers may be used from separate threads at once; one
+ * sampler, like the reference's, is not thread-safe.  greedy_sample and the two
+ * penalty functions take no sampler and share one lazily created per-process
+ * context guarded by a mutex.
  */
 #ifndef SAMPLER_H
 #define SAMPLER_H
@@ -46,9 +48,10 @@ void sampler_apply_presence_penalty(float *logits, int vocab_size, const int *se
                                     float presence_penalty);
 
 /* One token from the row (src/sampler.c:136-234); advances the rng state once
- * unless temperature == 0.  The row is not modified.  Returns -1 only when the
- * device call fails or the configuration is outside what the device path
- * implements (a negative or denormal-small temperature). */
+ * unless temperature == 0.  The row is not modified.  Every configuration of the
+ * reference is served (any non-zero temperature, any 0 < top_k < vocab_size).
+ * Returns -1 only when the device call fails, or for a row whose
+ * (l - max) / temperature holds NaN while top_k > 4096. */
 int sampler_sample(sampler *s, float *logits, int vocab_size);
 
 /* First index of the maximum; 0 when logits[0] is NaN (src/sampler.c:9-19). */
