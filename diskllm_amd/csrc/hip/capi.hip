@@ -255,51 +255,35 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     memset(&f, 0, sizeof(f));
     f.G = G;
     f.S = S;
-    f.stage_cap = 160;
+    f.stage_cap = 64;
     f.force_exact = force_exact;
-    /* carve order of full_kernel: sbits, spre, ce, cp, cbh, ca, rtot, rnext, rend, rpre, Pc, smap, svals, shalf, elist, pc,
-     * misc, md (then the prefetch buffers) */
-    size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
-                 4 * r16((size_t)nch * 4) + 2 * r16((size_t)nch * 8) + r16((size_t)(nch + 1) * 8) +
-                 r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) + 2 * r16((size_t)f.stage_cap * 8) + r16((size_t)G * kPubWords * 8) +
-                 r16(64 * 4) + r16(16 * 8);
+    /* carve order of full_kernel: sbits, spre, ce, cp, cbh, ca, rtot, rend, rpre, Pc, smap, svals, elist, seg,
+     * tab, tbase, rres, rbase, pc, misc, md */
+    const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
+                       2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
+                       r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) +
+                       r16((size_t)nch * 8) + r16((size_t)nch * 16) + r16((size_t)kMaxTabs * 64 * 8) +
+                       r16((size_t)kMaxTabs * 4) + r16((size_t)(kFullThreads / 64) * 64 * 8) +
+                       r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
     if (lds > kMaxLds) return 1;
-    /* workgroup 0 prefetches later slices' walk data into what LDS is left */
-    {
-        const int pf_cap = 32;
-        const size_t per = r16((size_t)nch * 16) + r16((size_t)pf_cap * 64 * 4) + 2 * r16((size_t)pf_cap * 8) + 16;
-        const size_t room = kMaxLds - lds;
-        int npf = (int)(room / per);
-        if (npf > G - 1) npf = G - 1;
-        if (npf > 32) npf = 32;
-        f.pf_slices = npf;
-        f.pf_cap = pf_cap;
-        lds += r16((size_t)npf * nch * 16) + r16((size_t)npf * pf_cap * 64 * 4) + 2 * r16((size_t)npf * pf_cap * 8) +
-               r16((size_t)npf * 4);
-    }
     int cap = dlk_full_kernel_capacity(ept, lds);
     int rows_per = cap / G;
     if (rows_per < 1) return 1;
     if (rows_per > rows) rows_per = rows;
     const size_t fb_bytes = r16(aggs_bytes(vocab));
     const size_t n_cv = r16((size_t)rows_per * G * kCandSlots * 64 * 4);
-    const size_t n_wr = r16((size_t)rows_per * G * nch * 16);
-    const size_t n_wv = r16((size_t)rows_per * G * f.stage_cap * 64 * 4);
-    const size_t n_wh = r16((size_t)rows_per * G * f.stage_cap * 8);      /* first-half sums; then the lists */
+    const size_t n_ln = r16((size_t)rows_per * G * kLaneWords * 8);
     WsView ws;
     /* the published words live in the zeroed counter region: they are zero
      * between launches (the kernel returns them to zero) */
     if (!workspace(stream, 0, (size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
-                   n_cv + n_wr + n_wv + 2 * n_wh + (size_t)rows_per * fb_bytes, ws))
+                   n_cv + n_ln + (size_t)rows_per * fb_bytes, ws))
         return g_ws_err;
     f.sync = ws.counters;
     f.pub = (uint64_t *)(ws.counters + (size_t)rows_per * kSyncWords);
     f.cvals = (float *)ws.data;
-    f.wrecs = (int4 *)(ws.data + n_cv);
-    f.wsvals = (float *)(ws.data + n_cv + n_wr);
-    f.wshalf = (double *)(ws.data + n_cv + n_wr + n_wv);
-    f.wel = (int2 *)(ws.data + n_cv + n_wr + n_wv + n_wh);
-    f.fb = ws.data + n_cv + n_wr + n_wv + 2 * n_wh;
+    f.lanes = (uint64_t *)(ws.data + n_cv);
+    f.fb = ws.data + n_cv + n_ln;
     f.fb_bytes = fb_bytes;
     for (int r0 = 0; r0 < rows; r0 += rows_per) {
         const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;

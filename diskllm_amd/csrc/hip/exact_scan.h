@@ -48,6 +48,7 @@ namespace dlk {
 constexpr uint64_t kCap = 1ull << 62;       /* saturation: far above any binade */
 constexpr int kInvalidBinade = 0x7fff;
 constexpr int kEmptyRun = 0x7ffe;          /* walk_pairs: consecutive element chunks */
+constexpr int kZeroBinade = 0x7ffd;        /* a chunk that adds nothing to the running value */
 
 struct Pair {
     uint64_t a0, a1;

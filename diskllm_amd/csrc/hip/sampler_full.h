@@ -17,10 +17,7 @@ constexpr int kSyncWords = 64;       /* per-row synchronisation words */
 /* per-row sync words (all zero between launches) */
 enum : int {
     kSyncExit = 3,     /* workgroups finished */
-    kSyncDone = 4,     /* token written */
-    kSyncChain = 16,   /* + w: running value for workgroup w is ready */
-    kSyncChainVal = 32,/* + w: that running value (float bits) */
-    kSyncWalk = 48     /* + w: walk data of slice w published for workgroup 0 */
+    kSyncLanes = 5     /* workgroups that published their candidate chains */
 };
 
 /* published words per workgroup */
@@ -32,26 +29,24 @@ enum : int {
     kPubCandChunk = 4, /* + s: global chunk index */
     kPubCandPre = 6,   /* + s: double, slice-local exclusive p prefix at that chunk */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
-    kPubStaged = 9,    /* staged chunks in the published walk data */
-    kPubNElem = 10,    /* entries of the published element-chunk list */
+    kPubF = 9          /* double: the slice's predicted contribution to the draw's float sum */
 };
+
+constexpr int kMaxTabs = 48;         /* element-level chunks with a candidate table per workgroup */
+constexpr int kLaneWords = 65;       /* per workgroup: 64 candidate chain results + the window base */
 
 struct FullParams {
     RowParams p;
     int G;             /* workgroups per row */
     int S;             /* slice length = EPT * kFullThreads */
     int stage_cap;     /* chunks of final probabilities kept in LDS per workgroup */
-    int pf_slices;     /* later slices whose walk data workgroup 0 prefetches into LDS */
-    int pf_cap;        /* staged chunks of a prefetched slice that fit its buffer */
     uint32_t *sync;    /* [rows][kSyncWords] */
     uint64_t *pub;     /* [rows][G][kPubWords], in the zeroed counter region: a word that readers
                           poll carries kReady (bit 63) once written; all zero between launches */
     float *cvals;      /* [rows][G][kCandSlots][64] */
-    int4 *wrecs;       /* [rows][G][nch]: each chunk's walk record (make_rec in exact_scan.h), stored as
-                          two arrays of 64-bit halves {x | y << 32}[nch] then {z | w << 32}[nch] */
-    float *wsvals;     /* [rows][G][stage_cap * 64]: staged chunks */
-    double *wshalf;    /* [rows][G][stage_cap]: first-half sum of each staged chunk */
-    int2 *wel;         /* [rows][G][stage_cap]: element-level chunks {chunk, slot} in order */
+    uint64_t *lanes;   /* [rows][G][kLaneWords]: per candidate start of the slice, its end value
+                          (low word) and crossing token (high word: -1 none, -2 unresolved);
+                          word 64: float bits of candidate 0 */
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;
     int force_exact;   /* test hook: send every row through the exact fallback */

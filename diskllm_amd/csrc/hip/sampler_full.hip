@@ -4,9 +4,10 @@
  *
  * A row is split over G workgroups, all resident at once (see
  * dlk_launch_full_kernel); each keeps its slice in registers.  The row is
- * tied together by three row barriers and a chain, all through relaxed
- * agent-scope atomics (every shared word is an atomic store/load; each writer
- * waits for its stores before it signals, so no cache-flushing fences are needed):
+ * tied together by four row barriers through relaxed agent-scope atomics
+ * (every shared word is an atomic store/load; each writer waits for its stores
+ * before it signals, so no cache-flushing fences are needed), and finished by
+ * the last workgroup to arrive:
  *
  *   A  slice maxima            -> M (src/sampler.c:155-158)
  *   B  slice sums of e         -> inv = (float)(1/sum), certified: the sequential
@@ -17,14 +18,17 @@
  *   C  slice sums of p and the few chunks that can hold the top-p crossing
  *                              -> every workgroup computes the same certified cut x
  *                                 and inv3 (:207-220)
- *   chain  each workgroup walks its slice with the exact float running sum of the
- *          draw (:226-232, exact_scan.h), starting from its predecessor's exact
- *          value, and hands its end value on; the one that crosses r writes the
- *          token.
+ *   D  each slice's predicted contribution to the draw's float running sum
+ *                              -> each workgroup's predicted exact start value
+ *   last  every workgroup runs the draw's exact float running sum (:226-232,
+ *         exact_scan.h) over its slice for 64 candidate start values around its
+ *         prediction; the last workgroup of the row composes the slices from the
+ *         row's exact start 0 and writes the token.
  *
  * Rows whose sums cannot be certified (the bound straddles a float rounding
- * boundary; probability ~1e-3 per row) are finished by workgroup 0 alone with the
- * exact sequential emulation of every sum (the general pipeline).
+ * boundary; probability ~1e-3 per row), or whose exact start value falls
+ * outside a slice's candidates, are finished by one workgroup with the exact
+ * sequential emulation of every sum (the general pipeline).
  */
 #include "sampler_common.h"
 #include "sampler_full.h"
@@ -43,43 +47,6 @@ DLK_DEV uint64_t at_ld64(const uint64_t *a) {
 }
 
 
-constexpr int kPfSkip = 0x100;                     /* prefetch: the group left the slice to the walk */
-
-/* Copies a slice's published walk data (records, staged values and their
- * first-half sums, element-chunk list) into LDS; each thread issues its
- * agent-scope loads before its LDS writes. */
-__device__ __forceinline__ void fetch_walk_data(const uint64_t *wr, const uint64_t *wv, const uint64_t *wh,
-                                                const uint64_t *we, int nch, int nst, int ne, int4 *rec, float *vals,
-                                                double *half, int2 *el, int tt, int TT) {
-    for (int i0 = 0; i0 < max(nst, ne); i0 += TT) {
-        const int i = i0 + tt;
-        const uint64_t h = i < nst ? at_ld64(&wh[i]) : 0, e = i < ne ? at_ld64(&we[i]) : 0;
-        if (i < nst) half[i] = u2d(h);
-        if (i < ne) el[i] = make_int2((int)(uint32_t)e, (int)(uint32_t)(e >> 32));
-    }
-    for (int c0 = 0; c0 < nch; c0 += 2 * TT) {
-        const int ca = c0 + tt, cb = c0 + TT + tt;
-        uint64_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-        if (ca < nch) { a0 = at_ld64(&wr[ca]); a1 = at_ld64(&wr[nch + ca]); }
-        if (cb < nch) { b0 = at_ld64(&wr[cb]); b1 = at_ld64(&wr[nch + cb]); }
-        if (ca < nch) rec[ca] = make_int4((int)a0, (int)(a0 >> 32), (int)a1, (int)(a1 >> 32));
-        if (cb < nch) rec[cb] = make_int4((int)b0, (int)(b0 >> 32), (int)b1, (int)(b1 >> 32));
-    }
-    uint64_t *v2 = (uint64_t *)vals;
-    for (int i0 = 0; i0 < nst * 32; i0 += 4 * TT) {
-        uint64_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int i = i0 + k * TT + tt;
-            w[k] = i < nst * 32 ? at_ld64(&wv[i]) : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int i = i0 + k * TT + tt;
-            if (i < nst * 32) v2[i] = w[k];
-        }
-    }
-}
 
 /* Issues the loads of a slice: 16-byte groups of logits (an out-of-range group
  * reads the slice start instead) and, with a mask, each group's mask word. */
@@ -225,33 +192,6 @@ DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     return base + inc;
 }
 
-/* Element values of the draw inside one slice: staged chunks from LDS, anything
- * else recomputed from the logits exactly as the registers held it. */
-struct QSlice {
-    const int *smap;
-    const float *svals;
-    const float *lg;
-    const uint32_t *mk;
-    const uint32_t *sbits;
-    const uint32_t *spre;
-    const float *pval;           /* penalised value of each patched id */
-    int s0, x, topp;
-    float M, inv_t, inv, inv3;
-    const uint64_t *tab;
-    DLK_DEV float operator()(int i) const {
-        int sl = smap[i >> 6];
-        if (sl >= 0) return svals[sl * 64 + (i & 63)];
-        const int gi = s0 + i;
-        if (gi > x) return 0.0f;
-        float l = lg[gi];
-        if (mk && !((mk[gi >> 5] >> (gi & 31)) & 1u)) l = -INFINITY;
-        if ((sbits[i >> 5] >> (i & 31)) & 1u) l = pval[slice_rank(sbits, spre, i)];
-        float e = dlk_expf_glibc((l - M) * inv_t, tab);
-        float pj = e * inv;
-        return topp ? pj * inv3 : pj;
-    }
-};
-
 template <int EPT>
 __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -273,29 +213,25 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     unsigned char *q = L.region;
     uint32_t *sbits = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
     uint32_t *spre = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
-    double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);
+    double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);      /* e prefix; later the contributions' prefix */
     double *cp = (double *)carve(q, (size_t)(nch + 1) * 8);
-    int *cbh = (int *)carve(q, (size_t)nch * 4);                 /* chunk binade or kInvalidBinade */
+    int *cbh = (int *)carve(q, (size_t)nch * 4);                 /* chunk binade, kInvalidBinade or kZeroBinade */
     uint32_t *ca = (uint32_t *)carve(q, (size_t)nch * 4);        /* chunk increments on that grid */
     uint64_t *rtot = (uint64_t *)carve(q, (size_t)nch * 8);      /* increments to the end of the run */
-    int *rnext = (int *)carve(q, (size_t)nch * 4);               /* first chunk after the run */
-    int *rend = (int *)carve(q, (size_t)nch * 4);                /* scratch: last chunk of run r */
+    int *rend = (int *)carve(q, (size_t)nch * 4);                /* scratch: last chunk of segment s */
     uint64_t *rpre = (uint64_t *)carve(q, (size_t)nch * 8);      /* scratch: increments up to it */
     double *Pc = (double *)carve(q, (size_t)(nch + 1) * 8);      /* predicted running value */
-    int *smap = (int *)carve(q, (size_t)nch * 4);
+    int *smap = (int *)carve(q, (size_t)nch * 4);                /* staged slot of each chunk or -1 */
     float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
-    double *shalf = (double *)carve(q, (size_t)f.stage_cap * 8);  /* first-half sum of each staged chunk */
-    int2 *elist = (int2 *)carve(q, (size_t)f.stage_cap * 8);      /* element-level chunks {chunk, slot} */
+    int2 *elist = (int2 *)carve(q, (size_t)nch * 8);             /* element-level chunks {chunk, slot} */
+    int4 *seg = (int4 *)carve(q, (size_t)nch * 16);              /* the draw's segments */
+    int2 *tab = (int2 *)carve(q, (size_t)kMaxTabs * 64 * 8);     /* candidate tables {end bits, crossing} */
+    uint32_t *tbase = (uint32_t *)carve(q, (size_t)kMaxTabs * 4);  /* each table's first candidate */
+    int2 *rres = (int2 *)carve(q, (size_t)(kFullThreads / 64) * 64 * 8);   /* each wave's range: {end bits, token} */
+    uint32_t *rbase = (uint32_t *)carve(q, (size_t)(kFullThreads / 64) * 4);  /* each range's first candidate */
     uint64_t *pc = (uint64_t *)carve(q, (size_t)G * kPubWords * 8);   /* published words, cached */
     int *misc = (int *)carve(q, 64 * 4);
     double *md = (double *)carve(q, 16 * 8);
-    /* workgroup 0: walk data of later slices, prefetched while it walks its own */
-    const int npf = g == 0 ? f.pf_slices : 0;
-    int4 *pf_rec = (int4 *)carve(q, (size_t)npf * nch * 16);
-    float *pf_vals = (float *)carve(q, (size_t)npf * f.pf_cap * 64 * 4);
-    double *pf_shalf = (double *)carve(q, (size_t)npf * f.pf_cap * 8);
-    int2 *pf_el = (int2 *)carve(q, (size_t)npf * f.pf_cap * 8);
-    int *pf_ne = (int *)carve(q, (size_t)npf * 4);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
     /* ---- history first: the ids, and for an id inside this slice its logit
@@ -653,31 +589,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         __syncthreads();
     }
 
-    if (!ok) {
-        /* ---- exact fallback: workgroup 0 runs every sum sequentially-exact -- */
-        if (g == 0) {
-            int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
-            Row R;
-            R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np_row; R.pflag = L.pflag;
-            R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab;
-            FullBase fb{&R};
-            Scal Sc;
-            int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
-            if (t == 0) p.out_ids[row] = pos;
-            for (int j = t; j < n_out; j += T) {
-                int64_t o = (int64_t)row * n_out + j;
-                float pj = fb.e(j) * Sc.inv;
-                QDraw<FullBase> qd{&fb, &Sc};
-                float fj = qd(j);
-                if (p.out_cand_ids) p.out_cand_ids[o] = j;
-                if (p.out_cand_probs) p.out_cand_probs[o] = pj;
-                if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
-            }
-        }
-        row_exit(sync, pubrow, G);
-        return;
-    }
-
+    bool run_exact = !ok && g == 0;        /* the row's sums could not be certified */
+    if (ok) {
     /* ---- final probabilities, draw aggregates, staged chunks -------------- */
     double RWg = 0.0;
     for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
@@ -704,15 +617,21 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int cx = (x - s0) >> 6;
         Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + cp[min(nch, cx + 1)]);
     }
-    /* with each chunk's predicted binade: the binade of its start value when
-     * its end value has the same one, else kInvalidBinade */
+    /* each chunk's predicted binade: that of its start value when it and its
+     * end value, widened by a margin far beyond the float sum's accumulated
+     * rounding (2^-12 relative), share one; kInvalidBinade otherwise; and
+     * kZeroBinade for a chunk that adds nothing (every value 0, or absorbed by
+     * the double prefix, so certainly by the float sum) */
+    const double mu = 0x1p-12;
     for (int c = t; c <= nch; c += T) {
         const double a = fmin(RWg + cp[c], Rx) * scale;
         Pc[c] = a;
         if (c < nch) {
-            const int bh = predict_binade<24>(a);
-            const bool valid = bh == predict_binade<24>(fmin(RWg + cp[c + 1], Rx) * scale) && bh >= -100;
-            cbh[c] = valid ? bh : kInvalidBinade;
+            const double b = fmin(RWg + cp[c + 1], Rx) * scale;
+            const bool zero = cp[c + 1] == cp[c] || s0 + 64 * c > x;
+            const int bh = predict_binade<24>(a * (1.0 - mu));
+            const bool valid = bh == predict_binade<24>(b * (1.0 + mu)) && bh >= -100;
+            cbh[c] = zero ? kZeroBinade : valid ? bh : kInvalidBinade;
         }
     }
     __syncthreads();
@@ -732,11 +651,11 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int bh = kPreload ? pbh[j4] : cbh[c];
         /* the increments are integers below 2^24 wherever the prediction holds,
          * so their float sum is exact; where it does not the sum still reaches
-         * 2^24 (non-negative terms, monotone rounding) and the walk opens the
-         * chunk.  Computed for every lane (no branch: an invalid chunk's sum is
-         * not used, whatever its scale 2^(23 - kInvalidBinade) gives); a tie
-         * saturates the lane's sum, so a chunk whose total reaches 2^24 -- a
-         * tie, or a sum that leaves the binade -- is opened. */
+         * 2^24 (non-negative terms, monotone rounding) and the chunk becomes an
+         * element-level one.  Computed for every lane (no branch: an invalid or
+         * zero chunk's scale 2^(23 - bh) underflows to 0); a tie saturates the
+         * lane's sum, so a chunk whose total reaches 2^24 -- a tie, or a sum
+         * that leaves the binade -- is element-level. */
         float xs[4], n[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -750,15 +669,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         uint32_t sum = fr == 0.5f ? (1u << 25) : (uint32_t)fminf(fsum, 0x1p25f);
         sum = row_scan_u32(sum);
         if ((lane & 15) == 15) {
-            ca[c] = sum;
-            cbh[c] = (bh != kInvalidBinade && sum < (1u << 24)) ? bh : kInvalidBinade;
+            ca[c] = bh == kZeroBinade ? 0u : sum;
+            cbh[c] = (bh == kZeroBinade || (bh != kInvalidBinade && sum < (1u << 24))) ? bh : kInvalidBinade;
         }
     }
     if (t == 0) misc[10] = 0;
     __syncthreads();
-    /* runs: maximal stretches of valid chunks of one binade (nch <= T); and the
-     * position of each element-level chunk in the walk's list (the same scan,
-     * upper half-word) */
+    /* the draw's segments, in order: each maximal run of chunks of one binade
+     * (their values add exactly their increments on its grid), and each
+     * element-level chunk on its own.  One scan (nch <= T): increments in bits
+     * 0-39 (below 2^24 per chunk), segment ends in 40-51, element-level chunks
+     * in 52-63 (counts at most nch <= 4095).  seg[s] = {binade, first chunk,
+     * the run's increments (saturated at 2^24) or the chunk's table, next chunk}. */
     int elpos = -1;
     {
         const int c = t;
@@ -768,301 +690,279 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const bool end = in && (!vld || c == nch - 1 || cbh[c + 1] != bc);
         const uint64_t a = vld ? (uint64_t)ca[c] : 0;
         const bool isel = in && !vld;
-        /* one scan of three fields: increments (below 2^24 per chunk, so below
-         * 2^34 in all), run ends (bits 40-51) and element-level chunks (52-63),
-         * the counts at most nch <= 4095 */
         const uint64_t all = block_incl_prefix_u64(a | ((uint64_t)end << 40) | ((uint64_t)isel << 52),
                                                    (uint64_t *)L.red);
         const uint64_t ainc = all & ((1ull << 40) - 1);
         const uint32_t run = (uint32_t)((all >> 40) & 0xfffu) - (end ? 1u : 0u);
         if (isel) elpos = (int)(all >> 52) - 1;
-        if (t == T - 1) misc[17] = (int)(all >> 52);
+        if (t == T - 1) {
+            misc[17] = (int)(all >> 52);
+            misc[21] = (int)((all >> 40) & 0xfffu);
+        }
         if (end) { rend[run] = c; rpre[run] = ainc; }
         __syncthreads();
-        if (in) {
-            rnext[c] = vld ? rend[run] + 1 : c + 1;
-            rtot[c] = vld ? rpre[run] - (ainc - a) : 0;
+        if (in) rtot[c] = vld ? rpre[run] - (ainc - a) : 0;
+        if (end) {
+            if (vld) {
+                const int first = run == 0 ? 0 : rend[run - 1] + 1;
+                const uint64_t R = rpre[run] - (run == 0 ? 0ull : rpre[run - 1]);
+                seg[run] = make_int4(bc, first, (int)(R < (1ull << 24) ? R : (1ull << 24)), c + 1);
+            } else {
+                seg[run] = make_int4(kInvalidBinade, c, elpos, c + 1);
+            }
         }
     }
     __syncthreads();
-    /* chunks the walk may have to open: mispredicted or near a binade edge,
-     * near the draw threshold, holding x, or holding a tie; then the walk's
-     * record of every chunk (in the space of ce and cp, which are dead now) */
-    int4 *rec = (int4 *)ce;
-    const double vthr = (double)u2f(f2u(r) + 1u);
-    const double mu = 0x1p-9;
-    for (int c = t; c < nch; c += T) {
-        double a = Pc[c], b = Pc[c + 1];
-        bool want = cbh[c] == kInvalidBinade ||
-                    predict_binade<24>(a * (1.0 - mu)) != predict_binade<24>(b * (1.0 + mu)) ||
-                    (a * (1.0 - mu) <= vthr && vthr <= b * (1.0 + mu)) ||
-                    (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
+    /* each chunk's predicted contribution to the exact float running sum: its
+     * increments on its binade's grid (exact while the prediction holds), or
+     * the real sum of an element-level chunk (off by that chunk's rounding, a
+     * few of its ulps); the chunks staged in LDS: the element-level ones, the
+     * ones that may hold r's crossing, and x's */
+    double *fpre = ce;                             /* ce is free again */
+    const float thr_f = u2f(f2u(r) + 1u);          /* r < cumul  <=>  cumul >= thr_f */
+    const double vthr = (double)thr_f;
+    if (t < nch) {
+        const int c = t;
+        const int bh = cbh[c];
+        fpre[c] = bh != kInvalidBinade ? ldexp((double)ca[c], bh - 23) : Pc[c + 1] - Pc[c];
+        const double a = Pc[c], b = Pc[c + 1], m2 = 0x1p-9;
+        const bool want = bh == kInvalidBinade || (a * (1.0 - m2) <= vthr && vthr <= b * (1.0 + m2)) ||
+                          (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
         int sl = -1;
-        if (want && s0 + 64 * c < s1 && s0 + 64 * c <= x) {
+        if (want && s0 + 64 * c <= x) {
             sl = atomicAdd(&misc[10], 1);
-            if (sl >= f.stage_cap - 1) sl = -1;         /* the last slot is the walk's spare */
+            if (sl >= f.stage_cap) sl = -1;
         }
         smap[c] = sl;
-        rec[c] = make_rec(cbh[c], sl, rnext[c], rtot[c]);
-        if (elpos >= 0 && elpos < f.stage_cap) elist[elpos] = make_int2(c, sl);
+        if (elpos >= 0) elist[elpos] = make_int2(c, sl);
     }
     __syncthreads();
+    block_excl_scan(fpre, nch, L.red);             /* fpre[c]: before chunk c; fpre[nch]: the slice */
+    if (t == 0) at_st64(&mypub[kPubF], d2u(fpre[nch]) | kReady);
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T;
         const int sl = smap[u >> 4];
         if (sl >= 0)
-            for (int k = 0; k < 4; k++) svals[sl * 64 + (u & 15) * 4 + k] = v[4 * j4 + k];
-        if (ballot(sl >= 0) != 0) {
-            /* a chunk is one 16-lane row: the sum of its first 32 values */
-            double d = 0.0;
-            if ((u & 15) < 8)
-                d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
-            d = row_scan_d(d);
-            if (sl >= 0 && (lane & 15) == 15) shalf[sl] = d;
+            *(float4 *)&svals[sl * 64 + (u & 15) * 4] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+    }
+
+    /* ---- D: the slices' predicted contributions -> this slice's predicted
+     *      exact start value (exact for slice 0: the sum starts at 0) ------- */
+    {
+        const int idx[1] = {kPubF};
+        row_gather(pubrow, G, idx, pc, p.status);
+    }
+    double Phat = 0.0;
+    for (int h = 0; h < g; h++) Phat += u2d(pc[h * kPubWords + kPubF]);
+
+    /* ---- candidate tables: each element-level chunk summed in order from the
+     *      64 consecutive floats around its predicted start, one wave per chunk
+     *      (src/sampler.c:226-232); lane k keeps the end value and the first
+     *      position whose running value reaches thr_f ------------------------ */
+    const int ntab = min(misc[17], kMaxTabs);
+    for (int ti = wave_id(); ti < ntab; ti += T / 64) {
+        const int2 e = elist[ti];
+        uint32_t base = 0xffffffffu;
+        if (e.y >= 0) {
+            const uint32_t pb = f2u((float)(Phat + fpre[e.x]));
+            base = pb >= 32u ? pb - 32u : 0u;
+            float c = u2f(base + (uint32_t)lane);
+            int below = 0;
+            const float4 *q4 = (const float4 *)(svals + e.y * 64);
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float4 qv = q4[k];
+                c = c + qv.x;
+                below += c < thr_f ? 1 : 0;
+                c = c + qv.y;
+                below += c < thr_f ? 1 : 0;
+                c = c + qv.z;
+                below += c < thr_f ? 1 : 0;
+                c = c + qv.w;
+                below += c < thr_f ? 1 : 0;
+            }
+            tab[ti * 64 + lane] = make_int2((int)f2u(c), below < 64 ? below : -1);
         }
+        if (lane == 0) tbase[ti] = base;
     }
     __syncthreads();
-    /* the walk's list of element-level chunks (a slot of -1: not staged) */
-    const int n_el = min(misc[17], f.stage_cap);
 
-    /* ---- walk data of the later slices, published for workgroup 0 ------- */
-    if (g > 0) {
-        const int64_t rg = (int64_t)row * G + g;
-        /* agent-scope stores: the reader may sit on another XCD, whose L2 is not
-         * coherent with this one for plain stores */
-        uint64_t *wr = (uint64_t *)(f.wrecs + rg * nch);
-        uint64_t *wv = (uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64);
-        const int nst = min(misc[10], f.stage_cap - 1);
-        for (int c = t; c < nch; c += T) {
-            /* two arrays of halves, so that each store is contiguous across lanes */
-            const int4 rc = rec[c];
-            at_st64(&wr[c], (uint64_t)(uint32_t)rc.x | ((uint64_t)(uint32_t)rc.y << 32));
-            at_st64(&wr[nch + c], (uint64_t)(uint32_t)rc.z | ((uint64_t)(uint32_t)rc.w << 32));
+    /* ---- the slice's draw for 64 candidate start values (slice 0: its exact
+     *      start 0 in every lane).  The segments are split into one contiguous
+     *      range per wave; wave w runs its range for the 64 consecutive floats
+     *      around the range's predicted start, segment by segment: a run adds
+     *      its increments (exact while the value stays in the run's binade), an
+     *      element-level chunk is a table lookup.  A lane that leaves what the
+     *      prediction covers (another binade, a value outside a table, a crossing
+     *      in an unstaged chunk) is marked -2.  Wave 0 then composes the ranges:
+     *      each range's lane for the value the previous range ended with ------- */
+    const int nch_loc = x < s0 ? 0 : min(nch, ((x - s0) >> 6) + 1);
+    const int nseg = misc[21];
+    const int per = (nseg + T / 64 - 1) / (T / 64);
+    const int nrng = per > 0 ? (nseg + per - 1) / per : 0;
+    if (wave_id() < nrng) {
+        const int w = wave_id();
+        const int sa = w * per, sb = min(nseg, sa + per);
+        const int c0 = seg[sa].y;
+        const double pstart = Phat + fpre[c0];
+        uint32_t rb = 0, cb = 0;
+        if (g > 0 || w > 0) {
+            const uint32_t pb = f2u((float)pstart);
+            rb = pb >= 32u ? pb - 32u : 0u;
+            cb = rb + (uint32_t)lane;
         }
-        const uint64_t *sv2 = (const uint64_t *)svals;
-        for (int i = t; i < nst * 32; i += T) at_st64(&wv[i], sv2[i]);
-        uint64_t *wh = (uint64_t *)(f.wshalf + rg * f.stage_cap);
-        uint64_t *we = (uint64_t *)(f.wel + rg * f.stage_cap);
-        for (int i = t; i < nst; i += T) at_st64(&wh[i], d2u(shalf[i]));
-        for (int i = t; i < n_el; i += T) at_st64(&we[i], (uint64_t)(uint32_t)elist[i].x | ((uint64_t)(uint32_t)elist[i].y << 32));
-        if (t == 0) at_st64(&mypub[kPubNElem], (uint64_t)n_el);
-        if (t == 0) at_st64(&mypub[kPubStaged], (uint64_t)nst);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (t == 0) at_st32(&sync[kSyncWalk + g], 1u);
+        int tok = -1;                              /* -1 no crossing yet; >= 0 token; -2 unresolved */
+        if (c0 >= nch_loc) {
+            /* past x: every value is 0 and the range adds nothing */
+        } else if (pstart > vthr * (1.0 + 0x1p-9)) {
+            tok = -3;                              /* r's crossing lies before this range */
+        } else {
+            for (int s = sa; s < sb; s++) {
+                const int4 sg = seg[s];
+                const int sx = sg.x, sy = sg.y, sz = sg.z, sw = sg.w;
+                if (sy >= nch_loc || ballot(tok == -1) == 0) break;
+                if (tok != -1 || sx == kZeroBinade) continue;
+                if (sx != kInvalidBinade) {
+                    /* run [sy, sw) on the grid of binade sx: exact integer steps
+                     * on the value's bits while it stays in the binade */
+                    const uint32_t R = (uint32_t)sz;
+                    const bool inb = (cb >> 23) == (uint32_t)(sx + 127) && (cb & 0x7fffffu) + R < 0x800000u;
+                    if (!inb) {
+                        tok = -2;
+                    } else if (u2f(cb + R) >= thr_f) {
+                        /* the crossing is in this run: its chunk by bisection on
+                         * the increments to the run's end, then its element */
+                        const uint64_t R0 = rtot[sy];
+                        int lo = sy, hi = sw - 1;
+                        while (lo < hi) {
+                            const int mid = (lo + hi) >> 1;
+                            const uint64_t after = mid + 1 < sw ? rtot[mid + 1] : 0ull;
+                            if (u2f(cb + (uint32_t)(R0 - after)) >= thr_f) hi = mid;
+                            else lo = mid + 1;
+                        }
+                        const int sl = smap[lo];
+                        tok = -2;
+                        if (sl >= 0) {
+                            uint32_t m = cb + (uint32_t)(R0 - rtot[lo]);
+                            const float *qv = svals + sl * 64;
+                            for (int i = 0; i < 64; i++) {
+                                m += (uint32_t)rintf(ldexpf(qv[i], 23 - sx));
+                                if (u2f(m) >= thr_f) {
+                                    tok = s0 + 64 * lo + i;
+                                    break;
+                                }
+                            }
+                        }
+                    } else {
+                        cb += R;
+                    }
+                } else {
+                    /* element-level chunk sy: its table sz */
+                    const uint32_t bse = sz < ntab ? tbase[sz] : 0xffffffffu;
+                    const uint32_t d = cb - bse;
+                    if (bse == 0xffffffffu || d >= 64u) {
+                        tok = -2;
+                    } else {
+                        const int2 te = tab[sz * 64 + (int)d];
+                        if (te.y >= 0) tok = s0 + 64 * sy + te.y;
+                        else cb = (uint32_t)te.x;
+                    }
+                }
+            }
+        }
+        rres[w * 64 + lane] = make_int2((int)cb, tok);
+        if (lane == 0) rbase[w] = rb;
     }
-
-    /* ---- chain: exact draw, from the predecessor's exact value -------------
-     * Workgroup 0 walks its slice and then the later ones from their published
-     * walk data (no hand-off latency); a slice it cannot walk (an element-level
-     * chunk that was not staged) goes back to its owner, which walks it and
-     * hands on as the chain did before. */
-    float c_in = 0.0f;
-    if (g > 0) {
+    __syncthreads();
+    if (wave_id() == 0) {
+        uint32_t wbase = 0;
+        if (g > 0) {
+            const uint32_t pb = f2u((float)Phat);
+            wbase = pb >= 32u ? pb - 32u : 0u;
+        }
+        uint32_t cb = g > 0 ? wbase + (uint32_t)lane : 0u;
+        int tok = -1;
+        for (int w = 0; w < nrng; w++) {
+            if (ballot(tok == -1) == 0) break;
+            if (tok != -1) continue;
+            const uint32_t d = cb - rbase[w];
+            if (d >= 64u) {
+                tok = -2;
+            } else {
+                const int2 e = rres[w * 64 + (int)d];
+                if (e.y == -1) cb = (uint32_t)e.x;
+                else tok = e.y == -3 ? -2 : e.y;
+            }
+        }
+        uint64_t *lw = f.lanes + ((int64_t)row * G + g) * kLaneWords;
+        at_st64(&lw[lane], (uint64_t)cb | ((uint64_t)(uint32_t)tok << 32));
+        if (lane == 0) at_st64(&lw[64], (uint64_t)wbase);
+    }
+    /* the chains are stored before the count that announces them */
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&sync[kSyncLanes], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        misc[22] = old == (uint32_t)(G - 1);
+    }
+    __syncthreads();
+    if (misc[22]) {
+        /* ---- the last workgroup of the row composes the slices from the
+         *      row's exact start 0: slice h's lane for the value slice h-1 ended
+         *      with gives slice h's end value or the token ---------------------- */
+        uint64_t *ent = (uint64_t *)tab;
+        const uint64_t *lrow = f.lanes + (int64_t)row * G * kLaneWords;
+        for (int i = t; i < G * kLaneWords; i += T) ent[i] = at_ld64(&lrow[i]);
+        __syncthreads();
         if (t == 0) {
-            int state = 0;
-            uint32_t spins = 0;
-            while (true) {
-                if (at_ld32(&sync[kSyncDone])) { state = 2; break; }
-                if (at_ld32(&sync[kSyncChain + g])) { state = 1; break; }
-                if (++spins > kSpinLimit) {
-                    if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
-                    state = 2;
-                    break;
+            uint32_t cb = 0;
+            int token = -1;
+            bool fail = false;
+            for (int h = 0; h < G && h * S <= x; h++) {
+                uint32_t d = 0;
+                if (h > 0) {
+                    d = cb - (uint32_t)ent[h * kLaneWords + 64];
+                    if (d >= 64u) { fail = true; break; }
                 }
+                const uint64_t e = ent[h * kLaneWords + d];
+                const int tk = (int)(uint32_t)(e >> 32);
+                if (tk == -2) { fail = true; break; }
+                if (tk >= 0) { token = tk; break; }
+                cb = (uint32_t)e;
             }
-            misc[11] = state;
-            if (state == 1) misc[12] = (int)at_ld32(&sync[kSyncChainVal + g]);
+            /* nothing crossed r up to x: the last kept entry (src/sampler.c:233) */
+            if (!fail && token < 0) token = x;
+            misc[23] = fail ? -1 : token;
         }
         __syncthreads();
-        if (misc[11] != 1) {
-            row_exit(sync, pubrow, G);
-            return;
+        if (misc[23] >= 0) {
+            if (t == 0) p.out_ids[row] = misc[23];
+        } else {
+            run_exact = true;
         }
-        c_in = u2f((uint32_t)misc[12]);
     }
-    /* prefetch state of later slice k+1: finished waves of its group, or
-     * kPfSkip when the group leaves it to the walk */
-    int *pf_ok = misc + 32;
-    const int pf_nw = T / 64 - 1, pf_gsz = npf > 0 ? max(1, pf_nw / npf) : 1;
-    if (npf > 0 && t < 64)
-        for (int kk = t; kk < npf; kk += 64) pf_ok[kk] = 0;
-    for (int gw = g;;) {
-        const bool own = gw == g;
-        const int k = gw - 1;                      /* prefetch slot of a later slice */
-        const bool pre = !own && k < npf && pf_ok[k] == pf_gsz;
-        const int4 *w_rec = rec;
-        const float *w_vals = svals;
-        const double *w_half = shalf;
-        const int2 *w_el = elist;
-        int cur_ne = own ? n_el : 0;
-        if (pre) {
-            w_rec = pf_rec + k * nch;
-            w_vals = pf_vals + (int64_t)k * f.pf_cap * 64;
-            w_half = pf_shalf + (int64_t)k * f.pf_cap;
-            w_el = pf_el + (int64_t)k * f.pf_cap;
-            cur_ne = pf_ne[k];
+    }
+
+    if (run_exact) {
+        /* ---- exact fallback: one workgroup runs every sum sequentially-exact -- */
+        int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
+        Row R;
+        R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np_row; R.pflag = L.pflag;
+        R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab;
+        FullBase fb{&R};
+        Scal Sc;
+        int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
+        if (t == 0) p.out_ids[row] = pos;
+        for (int j = t; j < n_out; j += T) {
+            int64_t o = (int64_t)row * n_out + j;
+            float pj = fb.e(j) * Sc.inv;
+            QDraw<FullBase> qd{&fb, &Sc};
+            float fj = qd(j);
+            if (p.out_cand_ids) p.out_cand_ids[o] = j;
+            if (p.out_cand_probs) p.out_cand_probs[o] = pj;
+            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
         }
-        if (!own && !pre) {
-            /* slice gw's walk data into this workgroup's arrays */
-            if (t == 0) {
-                uint32_t spins = 0, ok = 1;
-                while (!at_ld32(&sync[kSyncWalk + gw]))
-                    if (++spins > kSpinLimit) {
-                        if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
-                        ok = 0;
-                        break;
-                    }
-                misc[11] = (int)ok;
-            }
-            __syncthreads();
-            if (!misc[11]) break;
-            const int64_t rg = (int64_t)row * G + gw;
-            const int nst = (int)at_ld64(&pubrow[gw * kPubWords + kPubStaged]);
-            cur_ne = (int)at_ld64(&pubrow[gw * kPubWords + kPubNElem]);
-            fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch), (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64),
-                            (const uint64_t *)(f.wshalf + rg * f.stage_cap), (const uint64_t *)(f.wel + rg * f.stage_cap),
-                            nch, nst, cur_ne, rec, svals, shalf, elist, t, T);
-        }
-        __syncthreads();
-        WalkState st;
-        {
-            uint64_t m64;
-            split(c_in, st.b, m64);
-            st.m = (uint32_t)m64;
-            st.j = 0;
-        }
-        bool handed = false;
-        for (int round = 0;; round++) {
-            if (wave_id() == 0) {
-                const int n_loc = min(min(V, gw * S + S), x + 1) - gw * S;
-                WalkOut o = round == 0 ? walk_pairs(n_loc, w_rec, w_vals, w_half, w_el, cur_ne, vthr, st)
-                                       : walk_recs(n_loc, w_rec, w_vals, vthr, st);
-                /* workgroup 0 goes straight on through the prefetched slices */
-                int gc = gw;
-                float cin = c_in;
-                if (round == 0 && own && g == 0)
-                    while (o.pos < 0 && o.need < 0 && gc + 1 < G && gc < npf && x >= min(V, gc * S + S)) {
-                        uint32_t spins = 0;
-                        int pf;
-                        while ((pf = sreadi(__hip_atomic_load(&pf_ok[gc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))) <
-                                   pf_gsz && ++spins < kSpinLimit) {
-                        }
-                        if (pf != pf_gsz) break;
-                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                        cin = o.value;
-                        gc++;
-                        WalkState s2;
-                        {
-                            uint64_t m64;
-                            split(cin, s2.b, m64);
-                            s2.m = (uint32_t)m64;
-                            s2.j = 0;
-                        }
-                        const int kk = gc - 1;
-                        const int n2 = min(min(V, gc * S + S), x + 1) - gc * S;
-                        o = walk_pairs(n2, pf_rec + kk * nch, pf_vals + (int64_t)kk * f.pf_cap * 64,
-                                       pf_shalf + (int64_t)kk * f.pf_cap, pf_el + (int64_t)kk * f.pf_cap, pf_ne[kk], vthr,
-                                       s2);
-                    }
-                if (lane == 0) {
-                    misc[13] = o.pos;
-                    misc[14] = (int)f2u(o.value);
-                    misc[15] = o.need;
-                    misc[18] = gc;
-                    misc[19] = (int)f2u(cin);
-                }
-            } else if (own && npf > 0 && round == 0) {
-                /* the other waves fetch the later slices' walk data meanwhile:
-                 * one group of waves per slice, all slices at once */
-                const int kk = (wave_id() - 1) / pf_gsz;
-                if (kk < npf) {
-                    const int gs = kk + 1, tt = t - 64 - kk * pf_gsz * 64, TT = pf_gsz * 64;
-                    bool ok = true;
-                    if (lane == 0) {
-                        uint32_t spins = 0;
-                        while (!at_ld32(&sync[kSyncWalk + gs]))
-                            if (++spins > kSpinLimit) { ok = false; break; }
-                    }
-                    ok = __shfl(ok ? 1 : 0, 0, 64) != 0;
-                    const int nst = ok ? (int)at_ld64(&pubrow[gs * kPubWords + kPubStaged]) : 0;
-                    const int ne = ok ? (int)at_ld64(&pubrow[gs * kPubWords + kPubNElem]) : 0;
-                    /* a slice that did not publish in time, or staged more than fits,
-                     * is fetched by the walk itself */
-                    if (ok && nst <= f.pf_cap && ne <= f.pf_cap) {
-                        const int64_t rg = (int64_t)row * G + gs;
-                        fetch_walk_data((const uint64_t *)(f.wrecs + rg * nch),
-                                        (const uint64_t *)(f.wsvals + rg * (int64_t)f.stage_cap * 64),
-                                        (const uint64_t *)(f.wshalf + rg * f.stage_cap),
-                                        (const uint64_t *)(f.wel + rg * f.stage_cap), nch, nst, ne, pf_rec + kk * nch,
-                                        pf_vals + (int64_t)kk * f.pf_cap * 64, pf_shalf + (int64_t)kk * f.pf_cap,
-                                        pf_el + (int64_t)kk * f.pf_cap, tt, TT);
-                        if (tt == 0) pf_ne[kk] = ne;
-                        /* this wave's part is in LDS before the count says so */
-                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                        if (lane == 0) atomicAdd(&pf_ok[kk], 1);
-                    } else if (lane == 0) {
-                        atomicOr(&pf_ok[kk], kPfSkip);
-                    }
-                }
-            }
-            __syncthreads();
-            gw = misc[18];
-            const int need = misc[15];
-            if (need < 0) break;
-            if (gw != g) {
-                /* a chunk of another slice that was not staged: hand the slice to
-                 * its owner with its exact starting value */
-                if (t == 0) {
-                    at_st32(&sync[kSyncChainVal + gw], (uint32_t)misc[19]);
-                    __builtin_amdgcn_s_waitcnt(0);
-                    at_st32(&sync[kSyncChain + gw], 1u);
-                }
-                handed = true;
-                break;
-            }
-            /* stage the chunk into the spare slot and resume the walk there */
-            const int spare = f.stage_cap - 1;
-            if (t < 64) {
-                const int n_loc = min(min(V, gw * S + S), x + 1) - gw * S;
-                QSlice qs{smap, svals, lg, mk, sbits, spre, L.pval, gw * S, x, topp ? 1 : 0, M, inv_t, inv, inv3, L.tab};
-                const int i = need * 64 + t;
-                const float val = i < n_loc ? qs(i) : 0.0f;
-                svals[spare * 64 + t] = val;
-            }
-            __syncthreads();
-            if (t == 0) {
-                smap[need] = spare;
-                rec[need].x = (rec[need].x & 0xffff) | (spare << 16);
-            }
-            __syncthreads();
-        }
-        if (handed) break;
-        const int s1w = min(V, gw * S + S);
-        const int pos = misc[13];
-        int token = -1;
-        if (pos >= 0) token = gw * S + pos;
-        else if (x < s1w) token = x;             /* nothing crossed r up to x: the last kept entry */
-        if (token >= 0) {
-            if (t == 0) {
-                p.out_ids[row] = token;
-                __builtin_amdgcn_s_waitcnt(0);
-                at_st32(&sync[kSyncDone], 1u);
-            }
-            break;
-        }
-        c_in = u2f((uint32_t)misc[14]);
-        if (g != 0 || gw + 1 >= G) {
-            /* a later workgroup walked its own slice: hand on to the next */
-            if (gw + 1 < G && t == 0) {
-                at_st32(&sync[kSyncChainVal + gw + 1], f2u(c_in));
-                __builtin_amdgcn_s_waitcnt(0);
-                at_st32(&sync[kSyncChain + gw + 1], 1u);
-            }
-            break;
-        }
-        gw++;
     }
     row_exit(sync, pubrow, G);
 }
@@ -1112,3 +1012,4 @@ extern "C" int dlk_full_kernel_capacity(int ept, size_t lds) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     return per_cu * cus;
 }
+
