@@ -257,33 +257,41 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     f.S = S;
     f.stage_cap = 64;
     f.force_exact = force_exact;
-    /* carve order of full_kernel: sbits, spre, ce, cp, cbh, ca, rtot, rend, rpre, Pc, smap, svals, elist, seg,
+    /* carve order of full_kernel: sbits, spre, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
      * tab, tbase, rres, rbase, pc, misc, md */
-    const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + 2 * r16((size_t)(nch + 1) * 8) +
+    const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
                        2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
-                       r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + r16((size_t)f.stage_cap * 64 * 4) +
+                       r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)f.stage_cap * 64 * 4) +
                        r16((size_t)nch * 8) + r16((size_t)nch * 16) + r16((size_t)kMaxTabs * 64 * 8) +
                        r16((size_t)kMaxTabs * 4) + r16((size_t)(kFullThreads / 64) * 64 * 8) +
                        r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
     if (lds > kMaxLds) return 1;
-    int cap = dlk_full_kernel_capacity(ept, lds);
+    /* resident workgroups of this instance: queried once per (device, ept, LDS) */
+    struct CapEntry { int dev, ept; size_t lds; int cap; };
+    static std::vector<CapEntry> cap_cache;
+    int dev = 0, cap = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
+    for (const auto &e : cap_cache)
+        if (e.dev == dev && e.ept == ept && e.lds == lds) { cap = e.cap; break; }
+    if (cap < 0) {
+        cap = dlk_full_kernel_capacity(ept, lds);
+        cap_cache.push_back(CapEntry{dev, ept, lds, cap});
+    }
     int rows_per = cap / G;
     if (rows_per < 1) return 1;
     if (rows_per > rows) rows_per = rows;
     const size_t fb_bytes = r16(aggs_bytes(vocab));
-    const size_t n_cv = r16((size_t)rows_per * G * kCandSlots * 64 * 4);
     const size_t n_ln = r16((size_t)rows_per * G * kLaneWords * 8);
     WsView ws;
     /* the published words live in the zeroed counter region: they are zero
      * between launches (the kernel returns them to zero) */
     if (!workspace(stream, 0, (size_t)rows_per * kSyncWords + (size_t)rows_per * G * kPubWords * 2,
-                   n_cv + n_ln + (size_t)rows_per * fb_bytes, ws))
+                   n_ln + (size_t)rows_per * fb_bytes, ws))
         return g_ws_err;
     f.sync = ws.counters;
     f.pub = (uint64_t *)(ws.counters + (size_t)rows_per * kSyncWords);
-    f.cvals = (float *)ws.data;
-    f.lanes = (uint64_t *)(ws.data + n_cv);
-    f.fb = ws.data + n_cv + n_ln;
+    f.lanes = (uint64_t *)ws.data;
+    f.fb = ws.data + n_ln;
     f.fb_bytes = fb_bytes;
     for (int r0 = 0; r0 < rows; r0 += rows_per) {
         const int nr = rows - r0 < rows_per ? rows - r0 : rows_per;

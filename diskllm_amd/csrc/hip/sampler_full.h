@@ -25,11 +25,10 @@ enum : int {
     kPubMax = 0,       /* float bits of the slice maximum */
     kPubE = 1,         /* double: slice sum of e */
     kPubP = 2,         /* double: slice sum of p */
-    kPubNCand = 3,     /* number of crossing-candidate chunks */
-    kPubCandChunk = 4, /* + s: global chunk index */
-    kPubCandPre = 6,   /* + s: double, slice-local exclusive p prefix at that chunk */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
-    kPubF = 9          /* double: the slice's predicted contribution to the draw's float sum */
+    kPubF = 9,         /* double: the slice's predicted contribution to the draw's float sum */
+    kPubX = 10         /* from the slice holding the top-p crossing: x (bits 0-30, 0x7fffffff: not
+                          certified) and the float bits of inv3 (bits 31-62) */
 };
 
 constexpr int kMaxTabs = 48;         /* element-level chunks with a candidate table per workgroup */
@@ -43,7 +42,6 @@ struct FullParams {
     uint32_t *sync;    /* [rows][kSyncWords] */
     uint64_t *pub;     /* [rows][G][kPubWords], in the zeroed counter region: a word that readers
                           poll carries kReady (bit 63) once written; all zero between launches */
-    float *cvals;      /* [rows][G][kCandSlots][64] */
     uint64_t *lanes;   /* [rows][G][kLaneWords]: per candidate start of the slice, its end value
                           (low word) and crossing token (high word: -1 none, -2 unresolved);
                           word 64: float bits of candidate 0 */

@@ -207,14 +207,12 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     uint32_t *sync = f.sync + (int64_t)row * kSyncWords;
     uint64_t *pubrow = f.pub + (int64_t)row * G * kPubWords;
     uint64_t *mypub = pubrow + (int64_t)g * kPubWords;
-    float *mycv = f.cvals + ((int64_t)row * G + g) * kCandSlots * 64;
 
     Lds L = make_lds(smem, p.plan);
     unsigned char *q = L.region;
     uint32_t *sbits = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
     uint32_t *spre = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
     double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);      /* e prefix; later the contributions' prefix */
-    double *cp = (double *)carve(q, (size_t)(nch + 1) * 8);
     int *cbh = (int *)carve(q, (size_t)nch * 4);                 /* chunk binade, kInvalidBinade or kZeroBinade */
     uint32_t *ca = (uint32_t *)carve(q, (size_t)nch * 4);        /* chunk increments on that grid */
     uint64_t *rtot = (uint64_t *)carve(q, (size_t)nch * 8);      /* increments to the end of the run */
@@ -223,6 +221,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double *Pc = (double *)carve(q, (size_t)(nch + 1) * 8);      /* predicted running value */
     int *smap = (int *)carve(q, (size_t)nch * 4);                /* staged slot of each chunk or -1 */
     float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
+    uint32_t *spx = (uint32_t *)carve(q, (size_t)f.stage_cap * 64 * 4);   /* staged run chunks: increment prefixes */
     int2 *elist = (int2 *)carve(q, (size_t)nch * 8);             /* element-level chunks {chunk, slot} */
     int4 *seg = (int4 *)carve(q, (size_t)nch * 16);              /* the draw's segments */
     int2 *tab = (int2 *)carve(q, (size_t)kMaxTabs * 64 * 8);     /* candidate tables {end bits, crossing} */
@@ -447,8 +446,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     float inv3 = 1.0f;
     int x = V - 1;
     const bool topp = p.topp_on;
+    double RWg = 0.0;                              /* exact-bounded p prefix before this slice */
     if (ok) {
-        /* ---- p, its sums, and the chunks that may hold the top-p crossing ---- */
+        /* ---- p and the slice's p total (double, any order) ------------------ */
 #pragma unroll
         for (int j = 0; j < EPT; j++) v[j] = v[j] * inv;
         if (g == 0 && n_out > 0 && (p.out_cand_ids || p.out_cand_probs)) {
@@ -462,138 +462,171 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 }
             }
         }
+        {
+            double ps = 0.0;
 #pragma unroll
-        for (int j4 = 0; j4 < EPT / 4; j4++) {
-            double d = (double)v[4 * j4] + (double)v[4 * j4 + 1] + (double)v[4 * j4 + 2] + (double)v[4 * j4 + 3];
-            d = row_scan_d(d);
-            if ((lane & 15) == 15) cp[(t + j4 * T) >> 4] = d;
-        }
-        __syncthreads();
-        block_excl_scan(cp, nch, L.red);
-        if (t == 0) misc[1] = 0;
-        __syncthreads();
-        uint64_t cw[5] = {0, 0, 0, 0, 0};          /* NCand, CandChunk 0/1, CandPre 0/1 */
-        const double tau = p.topp_thr;
-        if (topp && p.top_p > 0.0f) {
-            /* p-prefix predicted from the e-prefix: |p - e*inv| <= 2^-24 p each,
-             * the float chunk sums within 5 * 2^-24, inv within 2^-24 */
-            const double dl = 0x1p-20;
-            for (int c = t; c < nch; c += T) {
-                if (s0 + 64 * c >= s1) continue;
-                double lo = (double)inv * (EPw + ce[c]) * (1.0 - dl);
-                double hi = (double)inv * (EPw + ce[c + 1]) * (1.0 + dl);
-                if (lo <= tau && tau <= hi) {
-                    int s = atomicAdd(&misc[1], 1);
-                    if (s < kCandSlots) misc[2 + s] = c;
-                }
-            }
+            for (int j4 = 0; j4 < EPT / 4; j4++)
+                ps += ((double)v[4 * j4] + (double)v[4 * j4 + 1]) + ((double)v[4 * j4 + 2] + (double)v[4 * j4 + 3]);
+            ps = wave_incl_scan_d(ps);
+            if (lane == 63) L.red[wave_id()] = ps;
             __syncthreads();
-            int ncand = misc[1];
-            if (ncand > kCandSlots) {
-                cw[0] = 0xffffull;
-            } else {
-                if (ncand == 2 && misc[2] > misc[3] && t == 0) { int tmp = misc[2]; misc[2] = misc[3]; misc[3] = tmp; }
-                __syncthreads();
-                for (int s = 0; s < ncand; s++) {
-                    const int c = misc[2 + s];
-#pragma unroll
-                    for (int j4 = 0; j4 < EPT / 4; j4++) {
-                        const int u = t + j4 * T;                 /* 4-element group index */
-                        if ((u >> 4) == c)
-                            for (int k = 0; k < 4; k++)
-                                at_st32((uint32_t *)&mycv[s * 64 + (u & 15) * 4 + k], f2u(v[4 * j4 + k]));
-                    }
-                    cw[1 + s] = (uint64_t)(s0 / 64 + c);
-                    cw[3 + s] = d2u(cp[c]);
-                }
-                cw[0] = (uint64_t)ncand;
-            }
-        }
-        /* the candidate values are stored before the words that announce them */
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (t == 0) {
-            at_st64(&mypub[kPubP], d2u(cp[nch]) | kReady);
-            at_st64(&mypub[kPubP0], (g == 0 ? (uint64_t)f2u(v[0]) : 0ull) | kReady);
-            at_st64(&mypub[kPubNCand], cw[0] | kReady);
-            for (int k2 = 0; k2 < 2; k2++) {
-                at_st64(&mypub[kPubCandChunk + k2], cw[1 + k2] | kReady);
-                at_st64(&mypub[kPubCandPre + k2], cw[3 + k2] | kReady);
+            if (t == 0) {
+                double tot = 0.0;
+                for (int w2 = 0; w2 < T / 64; w2++) tot += L.red[w2];
+                at_st64(&mypub[kPubP], d2u(tot) | kReady);
+                at_st64(&mypub[kPubP0], (g == 0 ? (uint64_t)f2u(v[0]) : 0ull) | kReady);
             }
         }
 
-        /* ---- C: top-p cut and its normaliser ------------------------------ */
+        /* ---- C: the slices' p totals -> the top-p cut x and its normaliser
+         *      inv3 (src/sampler.c:205-220): the slice holding the crossing finds
+         *      and certifies them and hands them to the others ----------------- */
         {
-            const int idx[7] = {kPubP, kPubP0, kPubNCand, kPubCandChunk, kPubCandChunk + 1, kPubCandPre,
-                                kPubCandPre + 1};
+            const int idx[2] = {kPubP, kPubP0};
             row_gather(pubrow, G, idx, pc, p.status);
         }
-        /* every workgroup's candidate chunks (svals is free until the staging):
-         * slots that turn out unused are simply not looked at */
-        float *cvl = svals;
-        for (int i = t; i < G * kCandSlots * 64; i += T)
-            cvl[i] = u2f(at_ld32((const uint32_t *)(f.cvals + (int64_t)row * G * kCandSlots * 64 + i)));
-        __syncthreads();
-        if (wave_id() == 0) {
-            /* one wave: each candidate chunk's running sum by a wave scan; any
-             * summation order is fine, the bound e covers the difference */
-            int okc = 1, xx = V - 1;
-            float i3 = 1.0f;
-            if (!topp) {
-                /* no renormalisation (src/sampler.c:205) */
-            } else if (p.top_p <= 0.0f) {
-                xx = 0;                                      /* cumul after the first entry */
-                i3 = (float)(1.0 / (double)u2f((uint32_t)pc[kPubP0]));
-            } else {
-                double RW = 0.0, s3 = 0.0, eps3 = 0.0;
+        for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
+        const double U = 0x1p-53;
+        int hx = -1;                               /* the slice that finds x */
+        if (!topp) {
+            /* no renormalisation (src/sampler.c:205) */
+        } else if (p.top_p <= 0.0f) {
+            x = 0;                                 /* cumul after the first entry */
+            inv3 = (float)(1.0 / (double)u2f((uint32_t)pc[kPubP0]));
+        } else {
+            /* the first slice whose end prefix may reach tau; |ours - sequential|
+             * within the bound e of the reference's double sum (src/sampler.c:209) */
+            const double tau = p.topp_thr;
+            double R = 0.0;
+            bool amb = false;
+            for (int h = 0; h < G && hx < 0; h++) {
+                R += u2d(pc[h * kPubWords + kPubP]);
+                const double e = ((double)min(V, (h + 1) * S) + 256.0) * U * 1.01 + 4.0 * U;
+                if (R * (1.0 + e) >= tau) {
+                    hx = h;
+                    amb = R * (1.0 - e) < tau;     /* the crossing may be at its very end or beyond */
+                }
+            }
+            if (hx < 0) {
+                /* the whole row stays below top_p: nk = k (src/sampler.c:208-215) */
+                const double e = ((double)V + 256.0) * U * 1.01 + 4.0 * U;
+                const float a = (float)(1.0 / (R * (1.0 + e))), b = (float)(1.0 / (R * (1.0 - e)));
+                if (a == b) inv3 = a;
+                else ok = false;
+            } else if (amb) {
+                ok = false;
+            }
+        }
+        if (ok && hx == g) {
+            /* this slice holds the crossing: the chunks that may hold it, from the
+             * e prefix (|p - e*inv| <= 2^-24 p each, the float chunk sums within
+             * 5 * 2^-24, inv within 2^-24) */
+            const double tau = p.topp_thr, dl = 0x1p-20;
+            if (t == 0) misc[1] = 0;
+            __syncthreads();
+            for (int c = t; c < nch; c += T) {
+                if (s0 + 64 * c >= s1) continue;
+                const double lo = RWg + (double)inv * ce[c] * (1.0 - dl);
+                const double hi = RWg + (double)inv * ce[c + 1] * (1.0 + dl);
+                if (lo <= tau && tau <= hi) {
+                    const int sl = atomicAdd(&misc[1], 1);
+                    if (sl < kCandSlots) misc[2 + sl] = c;
+                }
+            }
+            __syncthreads();
+            const int ncand = misc[1];
+            int okc = ncand >= 1 && ncand <= kCandSlots;
+            int c0 = okc ? misc[2] : 0, c1 = okc && ncand == 2 ? misc[3] : -1;
+            if (c1 >= 0 && c1 < c0) { const int tmp = c0; c0 = c1; c1 = tmp; }
+            /* each candidate's exact prefix: the slice's values before it, summed
+             * per thread and over the block; and its 64 values into LDS */
+            double m0 = 0.0, m1 = 0.0;
+            float *cv = svals;
+#pragma unroll
+            for (int j4 = 0; j4 < EPT / 4; j4++) {
+                const int u = t + j4 * T;           /* 4-element group index */
+                const double d = ((double)v[4 * j4] + (double)v[4 * j4 + 1]) + ((double)v[4 * j4 + 2] + (double)v[4 * j4 + 3]);
+                if (u < 16 * c0) m0 += d;
+                if (u < 16 * c1) m1 += d;
+                const int cg = u >> 4;
+                if (okc && (cg == c0 || cg == c1))
+                    *(float4 *)&cv[(cg == c0 ? 0 : 64) + (u & 15) * 4] =
+                        make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+            }
+            m0 = wave_incl_scan_d(m0);
+            m1 = wave_incl_scan_d(m1);
+            if (lane == 63) { L.red[wave_id()] = m0; L.red[32 + wave_id()] = m1; }
+            __syncthreads();
+            if (wave_id() == 0) {
+                double P0 = 0.0, P1 = 0.0;
+                for (int w2 = 0; w2 < T / 64; w2++) { P0 += L.red[w2]; P1 += L.red[32 + w2]; }
+                int xx = V - 1;
+                double s3 = 0.0, eps3 = 0.0;
                 bool found = false;
-                for (int h = 0; h < G && okc && !found; h++) {
-                    const uint64_t nc = pc[h * kPubWords + kPubNCand];
-                    if (nc == 0xffffull) { okc = 0; break; }
-                    for (int s = 0; s < (int)nc && okc && !found; s++) {
-                        const int cg = (int)pc[h * kPubWords + kPubCandChunk + s];
-                        const double R0 = RW + u2d(pc[h * kPubWords + kPubCandPre + s]);
-                        const float *vals = cvl + (h * kCandSlots + s) * 64;
-                        const int i = cg * 64 + lane;
-                        double R = i < V ? (double)vals[lane] : 0.0;
-                        R = wave_incl_scan_d(R) + R0;
-                        const double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
-                        const int fl = first_lane(ballot(i < V && R * (1.0 + e) >= tau));
-                        if (fl < 64) {
-                            const double Rf = u2d(readlane64(d2u(R), fl));
-                            const double ef = ((double)(cg * 64 + fl + 1) + 256.0) * U * 1.01 + 4.0 * U;
-                            if (Rf * (1.0 - ef) >= tau) { found = true; xx = cg * 64 + fl; s3 = Rf; eps3 = ef; }
-                            else okc = 0;
-                        }
+                for (int k = 0; k < 2 && okc && !found; k++) {
+                    const int cg = k == 0 ? c0 : c1;
+                    if (cg < 0) break;
+                    const int i = s0 + cg * 64 + lane;
+                    double Rv = i < V ? (double)cv[k * 64 + lane] : 0.0;
+                    Rv = wave_incl_scan_d(Rv) + RWg + (k == 0 ? P0 : P1);
+                    const double e = ((double)(i + 1) + 256.0) * U * 1.01 + 4.0 * U;
+                    const int fl = first_lane(ballot(i < V && Rv * (1.0 + e) >= tau));
+                    if (fl < 64) {
+                        const double Rf = u2d(readlane64(d2u(Rv), fl));
+                        const double ef = ((double)(s0 + cg * 64 + fl + 1) + 256.0) * U * 1.01 + 4.0 * U;
+                        if (Rf * (1.0 - ef) >= tau) { found = true; xx = s0 + cg * 64 + fl; s3 = Rf; eps3 = ef; }
+                        else okc = 0;
                     }
-                    RW += u2d(pc[h * kPubWords + kPubP]);
                 }
-                if (okc && !found) {
-                    double e = ((double)V + 256.0) * U * 1.01 + 4.0 * U;
-                    if (RW * (1.0 + e) < tau) { xx = V - 1; s3 = RW; eps3 = e; }
-                    else okc = 0;
-                }
+                float i3 = 1.0f;
+                if (!found) okc = 0;
                 if (okc) {
-                    float a = (float)(1.0 / (s3 * (1.0 + eps3)));
-                    float b = (float)(1.0 / (s3 * (1.0 - eps3)));
+                    const float a = (float)(1.0 / (s3 * (1.0 + eps3)));
+                    const float b = (float)(1.0 / (s3 * (1.0 - eps3)));
                     if (a == b) i3 = a;
                     else okc = 0;
                 }
+                if (lane == 0) {
+                    misc[8] = okc;
+                    misc[9] = xx;
+                    md[0] = (double)i3;
+                    /* x in bits 0-30 (0x7fffffff: not certified), inv3 in 31-62 */
+                    at_st64(&mypub[kPubX], (uint64_t)(okc ? (uint32_t)xx : 0x7fffffffu) |
+                                               ((uint64_t)f2u(i3) << 31) | kReady);
+                }
             }
-            if (lane == 0) { misc[8] = okc; misc[9] = xx; md[0] = (double)i3; }
+            __syncthreads();
+            ok = misc[8] != 0;
+            x = misc[9];
+            inv3 = (float)md[0];
+        } else if (ok && hx >= 0) {
+            /* another slice holds the crossing: its word (one wave polls, bounded) */
+            if (wave_id() == 0) {
+                uint64_t wv = 0;
+                uint32_t spins = 0;
+                const uint64_t *src = &pubrow[hx * kPubWords + kPubX];
+                while (!((wv = at_ld64(src)) & kReady)) {
+                    if (++spins > kSpinLimit) {
+                        if (lane == 0 && p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
+                        wv = kReady | 0x7fffffffull;
+                        break;
+                    }
+                }
+                if (lane == 0) misc[10] = (int)(uint32_t)(wv & 0x7fffffffull);
+                if (lane == 0) misc[11] = (int)(uint32_t)(wv >> 31);
+            }
+            __syncthreads();
+            const uint32_t xw = (uint32_t)misc[10];
+            ok = xw != 0x7fffffffu;
+            x = (int)xw;
+            inv3 = u2f((uint32_t)misc[11]);
+            __syncthreads();
         }
-        __syncthreads();
-        ok = misc[8] != 0;
-        x = misc[9];
-        inv3 = (float)md[0];
-        __syncthreads();
     }
 
     bool run_exact = !ok && g == 0;        /* the row's sums could not be certified */
     if (ok) {
     /* ---- final probabilities, draw aggregates, staged chunks -------------- */
-    double RWg = 0.0;
-    for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         const int i = s0 + 4 * (t + (j / 4) * T) + (j & 3);
@@ -615,7 +648,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     {
         /* p prefix at x: bounded by the prefix at the end of x's chunk */
         int cx = (x - s0) >> 6;
-        Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + cp[min(nch, cx + 1)]);
+        Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + (double)inv * ce[min(nch, cx + 1)]);
     }
     /* each chunk's predicted binade: that of its start value when it and its
      * end value, widened by a margin far beyond the float sum's accumulated
@@ -624,11 +657,11 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      * the double prefix, so certainly by the float sum) */
     const double mu = 0x1p-12;
     for (int c = t; c <= nch; c += T) {
-        const double a = fmin(RWg + cp[c], Rx) * scale;
+        const double a = fmin(RWg + (double)inv * ce[c], Rx) * scale;
         Pc[c] = a;
         if (c < nch) {
-            const double b = fmin(RWg + cp[c + 1], Rx) * scale;
-            const bool zero = cp[c + 1] == cp[c] || s0 + 64 * c > x;
+            const double b = fmin(RWg + (double)inv * ce[c + 1], Rx) * scale;
+            const bool zero = ce[c + 1] == ce[c] || s0 + 64 * c > x;
             const int bh = predict_binade<24>(a * (1.0 - mu));
             const bool valid = bh == predict_binade<24>(b * (1.0 + mu)) && bh >= -100;
             cbh[c] = zero ? kZeroBinade : valid ? bh : kInvalidBinade;
@@ -739,12 +772,26 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     __syncthreads();
     block_excl_scan(fpre, nch, L.red);             /* fpre[c]: before chunk c; fpre[nch]: the slice */
     if (t == 0) at_st64(&mypub[kPubF], d2u(fpre[nch]) | kReady);
+    /* a staged chunk's values, and for a chunk of a run the inclusive prefix of
+     * its increments on the run's grid (a chunk is one 16-lane row) */
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T;
-        const int sl = smap[u >> 4];
-        if (sl >= 0)
-            *(float4 *)&svals[sl * 64 + (u & 15) * 4] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+        const int c = u >> 4;
+        const int sl = smap[c];
+        if (ballot(sl >= 0) != 0) {
+            const int bh = cbh[c];
+            const bool run = bh != kInvalidBinade && bh != kZeroBinade;
+            uint32_t n[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) n[k] = run ? (uint32_t)rintf(ldexpf(v[4 * j4 + k], 23 - bh)) : 0u;
+            const uint32_t s4 = ((n[0] + n[1]) + n[2]) + n[3];
+            const uint32_t ex = row_scan_u32(s4) - s4;
+            if (sl >= 0) {
+                *(float4 *)&svals[sl * 64 + (u & 15) * 4] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+                *(uint4 *)&spx[sl * 64 + (u & 15) * 4] = make_uint4(ex + n[0], ex + n[0] + n[1], ex + n[0] + n[1] + n[2], ex + s4);
+            }
+        }
     }
 
     /* ---- D: the slices' predicted contributions -> this slice's predicted
@@ -844,15 +891,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                         const int sl = smap[lo];
                         tok = -2;
                         if (sl >= 0) {
-                            uint32_t m = cb + (uint32_t)(R0 - rtot[lo]);
-                            const float *qv = svals + sl * 64;
-                            for (int i = 0; i < 64; i++) {
-                                m += (uint32_t)rintf(ldexpf(qv[i], 23 - sx));
-                                if (u2f(m) >= thr_f) {
-                                    tok = s0 + 64 * lo + i;
-                                    break;
-                                }
+                            /* the first element whose running value (the chunk's
+                             * start plus its increment prefix, on one grid) reaches
+                             * thr_f: a bisection on the prefixes */
+                            const uint32_t need = f2u(thr_f) - (cb + (uint32_t)(R0 - rtot[lo]));
+                            const uint32_t *px = spx + sl * 64;
+                            int ea = 0, eb = 63;
+                            while (ea < eb) {
+                                const int em = (ea + eb) >> 1;
+                                if (px[em] >= need) eb = em;
+                                else ea = em + 1;
                             }
+                            tok = s0 + 64 * lo + ea;
                         }
                     } else {
                         cb += R;
