@@ -18,7 +18,7 @@
 extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t lds_bytes, hipStream_t stream);
 extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
-extern "C" int dlk_full_kernel_capacity(int ept, size_t lds);
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap);
 extern "C" int dlk_launch_prepare_rows(const float *src, int64_t ld, float *dst, int64_t dld, int rows, int vocab,
                                        const uint32_t *mask, int64_t mask_ld, const int32_t *mask_row, float cap,
                                        hipStream_t stream);
@@ -267,15 +267,16 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
                        r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
     if (lds > kMaxLds) return 1;
     /* resident workgroups of this instance: queried once per (device, ept, LDS) */
-    struct CapEntry { int dev, ept; size_t lds; int cap; };
+    struct CapEntry { int dev, ept; size_t lds; int softcap, cap; };
     static std::vector<CapEntry> cap_cache;
+    const int softcap = p.cap > 0.0f ? 1 : 0;
     int dev = 0, cap = -1;
     if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
     for (const auto &e : cap_cache)
-        if (e.dev == dev && e.ept == ept && e.lds == lds) { cap = e.cap; break; }
+        if (e.dev == dev && e.ept == ept && e.lds == lds && e.softcap == softcap) { cap = e.cap; break; }
     if (cap < 0) {
-        cap = dlk_full_kernel_capacity(ept, lds);
-        cap_cache.push_back(CapEntry{dev, ept, lds, cap});
+        cap = dlk_full_kernel_capacity(ept, lds, softcap);
+        cap_cache.push_back(CapEntry{dev, ept, lds, softcap, cap});
     }
     int rows_per = cap / G;
     if (rows_per < 1) return 1;
@@ -338,10 +339,10 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
     if (!greedy && !b->rng) return DLK_ERR_INVALID;
     const int max_hist = prm->max_history > 0 ? prm->max_history : 1024;
     const bool cap_on = prm->softcap > 0.0f;                    /* src/core/context.c:604 */
-    if (cap_on || (b->hist_off && pow2_at_least(max_hist, 64) > kHcapDirect)) {
-        /* the rows as sampler_sample would see them -- soft-cap, mask, penalties
-         * (src/core/sampler_api.c:51-61) -- in a scratch copy; then the sampling
-         * alone over the copy */
+    if (b->hist_off && pow2_at_least(max_hist, 64) > kHcapDirect) {
+        /* a history too long to stage in LDS: the rows as sampler_sample would
+         * see them -- soft-cap, mask, penalties (src/core/sampler_api.c:51-61) --
+         * in a scratch copy; then the sampling alone over the copy */
         if (rows > 65535) return DLK_ERR_UNSUPPORTED;
         const int64_t ldp = ((int64_t)vocab + 63) & ~(int64_t)63;
         WsView ws;
@@ -381,6 +382,7 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
     p.rep = prm->repeat_penalty; p.freq = prm->frequency_penalty; p.pres = prm->presence_penalty;
     p.order = prm->penalty_order;
     p.greedy = greedy;
+    p.cap = cap_on ? prm->softcap : 0.0f;          /* applied inside the sampling kernels */
     if (!p.greedy) {
         p.inv_temp = 1.0f / prm->temperature;                   /* src/sampler.c:154 */
         /* 1/T negative, zero or infinite: s = (l - max) * (1/T) may be NaN or +inf
@@ -407,7 +409,8 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
         else region = aggs_bytes(vocab);
     }
     size_t total = fixed + region;
-    if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on) && !p.s_general) {
+    /* (greedy under a cap: the row kernel, whose argmax is taken on the capped row) */
+    if (prm->path == DLK_PATH_AUTO && (p.greedy || p.topk_on) && !p.s_general && !(p.greedy && cap_on)) {
         int rc = launch_topk(p, rows, vocab, stream);
         if (rc <= 0) return rc;
     }

@@ -22,6 +22,7 @@
 #include "dlk_device.h"
 #include "exact_scan.h"
 #include "sampler_params.h"
+#include "tanhf_glibc.h"
 
 namespace dlk {
 
@@ -39,10 +40,14 @@ struct Row {
     const uint32_t *pflag;   /* bit per 64-element chunk holding a penalised id */
     float M, inv_t, maxv;
     const uint64_t *tab;
+    float cap;               /* > 0: the soft-cap, applied first */
 };
 
+/* The logit sampler_sample sees: soft-capped (src/core/context.c:873-876), then
+ * the mask's -INFINITY (src/core/grammar.c:285-305), then the penalties. */
 DLK_DEV float prepared(const Row &R, int i) {
     float x = R.lg[i];
+    if (R.cap > 0.0f) x = dlk_softcap_glibc(x, R.cap);
     if (R.mk && !((R.mk[i >> 5] >> (i & 31)) & 1u)) x = -INFINITY;
     if (R.np && ((R.pflag[i >> 11] >> ((i >> 6) & 31)) & 1u)) {
         int lo = 0, hi = R.np;
@@ -311,6 +316,7 @@ __device__ __forceinline__ int build_patches(const RowParams &p, int row, const 
         int id = L.pid[j];
         int cnt = (int)L.pval[j];
         float x = lg[id];
+        if (p.cap > 0.0f) x = dlk_softcap_glibc(x, p.cap);
         if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
         x = penalize(x, cnt, p);
         L.pval[j] = x;

@@ -192,7 +192,7 @@ DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     return base + inc;
 }
 
-template <int EPT>
+template <int EPT, bool CAP>
 __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
@@ -332,6 +332,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             x = lg[id];
             m = mk ? mk[id >> 5] : 0xffffffffu;
         }
+        if (CAP) x = dlk_softcap_glibc(x, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
         if (!((m >> (id & 31)) & 1u)) x = -INFINITY;
         L.pval[slot] = penalize(x, L.pcnt[slot], p);
     }
@@ -348,6 +349,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int i0 = s0 + 4 * (t + j4 * T);
         float xs[4] = {raw[j4].x, raw[j4].y, raw[j4].z, raw[j4].w};
+        if (CAP) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) xs[c] = dlk_softcap_glibc(xs[c], p.cap);
+        }
         if (i0 >= s1) xs[0] = xs[1] = xs[2] = xs[3] = -INFINITY;
         if (mk) {
             const uint32_t mw = mwd[j4] >> (i0 & 31);
@@ -429,12 +434,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int idx[1] = {kPubE};
         row_gather(pubrow, G, idx, pc, p.status);
     }
-    double Sapx = 0.0, EPw = 0.0;
-    for (int h = 0; h < G; h++) {
-        double e = u2d(pc[h * kPubWords + kPubE]);
-        if (h < g) EPw += e;
-        Sapx += e;
-    }
+    double Sapx = 0.0;
+    for (int h = 0; h < G; h++) Sapx += u2d(pc[h * kPubWords + kPubE]);
     /* |sequential - exact| <= V u sum; |ours - exact| <= 64 u sum (summation depth) */
     const double U = 0x1p-53;
     const double eps_s = ((double)V + 64.0) * U * 1.01 + 4.0 * U;
@@ -999,7 +1000,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
         Row R;
         R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np_row; R.pflag = L.pflag;
-        R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab;
+        R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
         FullBase fb{&R};
         Scal Sc;
         int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
@@ -1019,17 +1020,30 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
 
 }  // namespace dlk
 
+namespace {
+template <bool CAP>
+const void *full_fn(int which) {
+    using namespace dlk;
+    switch (which) {
+        case 0: return (const void *)full_kernel<16, CAP>;
+        case 1: return (const void *)full_kernel<24, CAP>;
+        case 2: return (const void *)full_kernel<32, CAP>;
+        case 3: return (const void *)full_kernel<40, CAP>;
+        default: return (const void *)full_kernel<48, CAP>;
+    }
+}
+int ept_index(int ept) { return ept == 16 ? 0 : ept == 24 ? 1 : ept == 32 ? 2 : ept == 40 ? 3 : ept == 48 ? 4 : -1; }
+}  // namespace
+
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
     using namespace dlk;
-    const void *fns[5] = {(const void *)full_kernel<16>, (const void *)full_kernel<24>, (const void *)full_kernel<32>,
-                          (const void *)full_kernel<40>, (const void *)full_kernel<48>};
-    static int set[5] = {0, 0, 0, 0, 0};
-    int which = ept == 16 ? 0 : ept == 24 ? 1 : ept == 32 ? 2 : ept == 40 ? 3 : ept == 48 ? 4 : -1;
+    static int set[2][5] = {{0, 0, 0, 0, 0}, {0, 0, 0, 0, 0}};
+    const int which = ept_index(ept), cap = f->p.cap > 0.0f ? 1 : 0;
     if (which < 0) return -1;
-    if (!set[which]) {
-        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-            return -1;
-        set[which] = 1;
+    const void *fn = cap ? full_fn<true>(which) : full_fn<false>(which);
+    if (!set[cap][which]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
+        set[cap][which] = 1;
     }
     /* An ordinary launch: the grid fits the device at one workgroup per CU
      * (checked by the host against dlk_full_kernel_capacity), and the row
@@ -1038,23 +1052,17 @@ extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ep
      * the dispatch frontier is fully resident and finishes, which frees room
      * for the rest: the barriers make progress without a cooperative launch
      * (which costs ~12 us of launch latency here), and every wait is bounded. */
-    const FullParams fp = *f;
-    switch (which) {
-        case 0: hipLaunchKernelGGL(full_kernel<16>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
-        case 1: hipLaunchKernelGGL(full_kernel<24>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
-        case 2: hipLaunchKernelGGL(full_kernel<32>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
-        case 3: hipLaunchKernelGGL(full_kernel<40>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
-        default: hipLaunchKernelGGL(full_kernel<48>, dim3(rows * f->G), dim3(kFullThreads), lds, stream, fp); break;
-    }
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? 0 : -1;
+    FullParams fp = *f;
+    void *args[] = {&fp};
+    if (hipLaunchKernel(fn, dim3(rows * f->G), dim3(kFullThreads), args, lds, stream) != hipSuccess) return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-extern "C" int dlk_full_kernel_capacity(int ept, size_t lds) {
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap) {
     using namespace dlk;
-    const void *fn = ept == 16 ? (const void *)full_kernel<16> : ept == 24 ? (const void *)full_kernel<24>
-                   : ept == 32 ? (const void *)full_kernel<32> : ept == 40 ? (const void *)full_kernel<40>
-                               : (const void *)full_kernel<48>;
+    const int which = ept_index(ept);
+    if (which < 0) return 0;
+    const void *fn = cap ? full_fn<true>(which) : full_fn<false>(which);
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return 0;
     int per_cu = 0, dev = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kFullThreads, lds) != hipSuccess) return 0;
@@ -1062,4 +1070,3 @@ extern "C" int dlk_full_kernel_capacity(int ept, size_t lds) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     return per_cu * cus;
 }
-

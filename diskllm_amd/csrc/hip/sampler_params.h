@@ -40,6 +40,7 @@ struct RowParams {
     uint32_t order;
     double topp_thr;     /* smallest double d with (float)d >= top_p */
     int greedy, topk_on, topp_on, minp_on;
+    float cap;           /* > 0: logits soft-capped, cap * tanhf(l / cap), before everything else */
     /* 1/temperature outside (0, inf): s = (l - max) * (1/T) may hold NaN or +inf
      * and its maximum is not 0 (row kernel only) */
     int s_general;

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
 
     Row R;
     R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np; R.pflag = L.pflag;
-    R.M = 0.0f; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab;
+    R.M = 0.0f; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
 
     /* max / argmax over the prepared row (src/sampler.c:9-19, :155-158) */
     float bv = -INFINITY;

@@ -20,6 +20,8 @@
 
 namespace dlk {
 
+constexpr float kFltMax = 3.40282347e38f;
+
 DLK_DEV uint32_t asc_key(float l) {          /* ascending orderable key, -0 == +0 */
     return ~desc_key(l);
 }
@@ -54,7 +56,14 @@ DLK_DEV float penalised(const RowParams &p, float x, int cnt) {
     return x;
 }
 
-template <int EPT>
+/* Soft-cap (CAP): y = cap * tanhf(x / cap) is non-decreasing in x (tanhf is
+ * non-decreasing from float to float: tests/native/tanhf_monotone_check.c), so a
+ * slice is streamed and thresholded on its raw logits -- with +-inf clamped to
+ * +-FLT_MAX, which the cap maps to the same +-cap -- and only the elements it
+ * collects are capped; the penalty patches are capped values, handled from
+ * their LDS list.  Ties that the cap creates are resolved by the order
+ * (y desc, index asc) of the collected candidates and the merge's certificate. */
+template <int EPT, bool CAP>
 __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
@@ -108,6 +117,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         }
         if (!first) continue;
         float x = lg[id];
+        if (CAP) x = dlk_softcap_glibc(x, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
         if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
         x = penalised(p, x, cnt);
         int at = atomicAdd(&misc[0], 1);
@@ -141,10 +151,15 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         for (int c = 0; c < 4; c++) {
             const int i = i0 + c;
             float x = xs[c];
+            if (CAP && !(x != x)) x = fminf(fmaxf(x, -kFltMax), kFltMax);   /* raw stand-in of cap(x) */
             if (!((mw >> c) & 1u)) x = -INFINITY;
             if ((pb >> c) & 1u) {
-                for (int k = 0; k < np; k++)
-                    if (L.pid[k] == i) x = L.pval[k];
+                if (CAP) {
+                    x = -INFINITY;                 /* a capped patch: from the LDS list below */
+                } else {
+                    for (int k = 0; k < np; k++)
+                        if (L.pid[k] == i) x = L.pval[k];
+                }
             }
             if (i >= s1) x = -INFINITY;
             v[j4 * 4 + c] = x;
@@ -155,12 +170,34 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
             }
         }
     }
+    float pmax = -INFINITY;                        /* CAP: largest capped patch */
+    if (CAP) {
+        for (int k = t; k < np; k += T) {
+            const float y = L.pval[k];
+            nfin += y > -INFINITY;
+            irr |= !(y < INFINITY) && !(y == -INFINITY);
+            pmax = fmaxf(pmax, y);
+        }
+    }
     /* ---- 3. workgroup max / argmax / finite count ----------------------- */
     float bm = tm;
     int bi = targ;
     block_argmax(bm, bi, L);
     int nf = block_sum_int(nfin, L);
     irr = block_sum_int(irr, L);
+    if (CAP) {
+        /* the slice maximum of the capped row (the argmax serves greedy
+         * sampling, which does not take this path under a cap) */
+        uint32_t pbits = asc_key(pmax);             /* ascending keys: the largest key is the maximum */
+        for (int m2 = 32; m2 >= 1; m2 >>= 1) pbits = max(pbits, (uint32_t)shfl_xor((int)pbits, m2));
+        if (lane == 0) misc[24 + w] = (int)pbits;
+        __syncthreads();
+        for (int u = 0; u < T / 64; u++) pbits = max(pbits, (uint32_t)misc[24 + u]);
+        __syncthreads();
+        const float pm = key_value(~pbits);
+        const float cm = bm > -INFINITY ? dlk_softcap_glibc(bm, p.cap) : bm;
+        bm = fmaxf(cm, pm);
+    }
     TopkSlot *slot = f.slots + ((int64_t)row * G + g);
     uint64_t *cands = f.cands + ((int64_t)row * G + g) * f.KP;
 
@@ -175,11 +212,15 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         const uint32_t thr_key = block_select_u32(T, T - min(KP, T), [&](int i) { return tk32[i]; }, selh, selh + 256);
         float thr = key_value(~thr_key);
         if (!(thr > -INFINITY)) thr = -INFINITY;
+        /* CAP: the patches at or above the capped threshold join the candidates */
+        const float cthr = CAP && thr > -INFINITY ? dlk_softcap_glibc(thr, p.cap) : -INFINITY;
         /* ---- 5. collect finite elements >= thr ------------------------- */
         /* a count per thread, one block prefix, then the writes */
         uint32_t cnt = 0;
 #pragma unroll
         for (int j = 0; j < EPT; j++) cnt += (v[j] > -INFINITY && v[j] >= thr) ? 1u : 0u;
+        if (CAP)
+            for (int k = t; k < np; k += T) cnt += (L.pval[k] > -INFINITY && L.pval[k] >= cthr) ? 1u : 0u;
         const uint32_t incl = wave_scan_sat_u32(cnt, 0xffffffffu);
         if (lane == 63) misc[8 + w] = (int)incl;
         __syncthreads();
@@ -192,8 +233,18 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         for (int j = 0; j < EPT; j++) {
             const float x = v[j];
             if (x > -INFINITY && x >= thr) {
-                if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(x) << 32) | (uint32_t)(s0 + 4 * (t + (j / 4) * T) + (j & 3));
+                const float y = CAP ? dlk_softcap_glibc(x, p.cap) : x;
+                if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)(s0 + 4 * (t + (j / 4) * T) + (j & 3));
                 at++;
+            }
+        }
+        if (CAP) {
+            for (int k = t; k < np; k += T) {
+                const float y = L.pval[k];
+                if (y > -INFINITY && y >= cthr) {
+                    if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)L.pid[k];
+                    at++;
+                }
             }
         }
         __syncthreads();
@@ -301,7 +352,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         /* NaN or +inf in the row: the reference's sequence on one thread */
         Row R;
         R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.pflag = L.pflag;
-        R.M = 0.0f; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab;
+        R.M = 0.0f; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
         R.np = build_patches(p, row, lg, mk, L, p.plan, V);
         if (t == 0) emulate_topk_row(p, R, k, r, buf, row);
         return;
@@ -314,7 +365,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
 
     Row R;
     R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = 0; R.pflag = L.pflag;
-    R.M = M; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab;
+    R.M = M; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
 
     /* gather candidates re-keyed on s, sorted (s desc, index asc) */
     bool ok = !overflow && total <= f.buf_cap;
@@ -478,25 +529,33 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
 
 }  // namespace dlk
 
+namespace {
+template <bool CAP>
+const void *topk_fn(int which) {
+    using namespace dlk;
+    switch (which) {
+        case 0: return (const void *)topk_kernel<4, CAP>;
+        case 1: return (const void *)topk_kernel<8, CAP>;
+        case 2: return (const void *)topk_kernel<16, CAP>;
+        case 3: return (const void *)topk_kernel<32, CAP>;
+        default: return (const void *)topk_kernel<64, CAP>;
+    }
+}
+}  // namespace
+
 extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
     using namespace dlk;
-    static int set[5] = {0, 0, 0, 0, 0};
-    const void *fns[5] = {(const void *)topk_kernel<4>, (const void *)topk_kernel<8>, (const void *)topk_kernel<16>,
-                          (const void *)topk_kernel<32>, (const void *)topk_kernel<64>};
-    int which = ept == 4 ? 0 : ept == 8 ? 1 : ept == 16 ? 2 : ept == 32 ? 3 : ept == 64 ? 4 : -1;
+    static int set[2][5] = {{0, 0, 0, 0, 0}, {0, 0, 0, 0, 0}};
+    const int which = ept == 4 ? 0 : ept == 8 ? 1 : ept == 16 ? 2 : ept == 32 ? 3 : ept == 64 ? 4 : -1;
+    const int cap = f->p.cap > 0.0f ? 1 : 0;
     if (which < 0) return -1;
-    if (!set[which]) {
-        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-            return -1;
-        set[which] = 1;
+    const void *fn = cap ? topk_fn<true>(which) : topk_fn<false>(which);
+    if (!set[cap][which]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
+        set[cap][which] = 1;
     }
-    dim3 grid(f->G, rows);
-    switch (which) {
-        case 0: hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(kTopkThreads), lds, stream, *f); break;
-        case 1: hipLaunchKernelGGL(topk_kernel<8>, grid, dim3(kTopkThreads), lds, stream, *f); break;
-        case 2: hipLaunchKernelGGL(topk_kernel<16>, grid, dim3(kTopkThreads), lds, stream, *f); break;
-        case 3: hipLaunchKernelGGL(topk_kernel<32>, grid, dim3(kTopkThreads), lds, stream, *f); break;
-        default: hipLaunchKernelGGL(topk_kernel<64>, grid, dim3(kTopkThreads), lds, stream, *f); break;
-    }
+    TopkParams fp = *f;
+    void *args[] = {&fp};
+    if (hipLaunchKernel(fn, dim3(f->G, rows), dim3(kTopkThreads), args, lds, stream) != hipSuccess) return -1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -101,8 +101,9 @@ int dlk_sample(const dlk_batch *batch, int rows, int vocab, const dlk_sample_par
  * device (held until the process ends), whose counter words each call clears
  * with a fill kernel on `stream`.  Every call on a device shares that device's
  * array, so calls that overlap on one device race.  DLK_ERR_UNSUPPORTED when the
- * call needs more than the array holds or a second buffer: softcap > 0,
- * max_history > 1024, or a batch whose kernels' workspace exceeds the array. */
+ * call needs more than the array holds or a second buffer: max_history > 1024
+ * (the penalties then run on a scratch copy of the rows), or a batch whose
+ * kernels' workspace exceeds the array. */
 #define DLK_NOALLOC_SCRATCH_BYTES (32u << 20)
 int dlk_sample_noalloc(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
                        hipStream_t stream);

@@ -499,6 +499,22 @@ def test_tanhf_restatement_vs_host_libm():
         assert checked > 1000000 and bad == 0, (extra, r.stdout, r.stderr[:500])
 
 
+def test_tanhf_monotone():
+    """tanhf (the restatement, bit-identical to the host libm) never decreases
+    from one float to the next, from -inf to +inf; hence x -> cap * tanhf(x / cap)
+    is non-decreasing for every cap > 0, which is what lets the top-k kernel
+    select soft-capped candidates on the raw logits.  Here every 97th pair of
+    consecutive floats, and the composite for two caps; the exhaustive run is the
+    same program with stride 1 (4,278,190,081 pairs, 0 decreases)."""
+    exe = os.path.join(ROOT, "oracle", "_build", "tanhf_monotone_check")
+    src = os.path.join(ROOT, "tests", "native", "tanhf_monotone_check.c")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm", "-lpthread"], check=True)
+    for extra, stride in (([], 97), (["cap=30"], 1021), (["cap=0.75"], 2039)):
+        r = subprocess.run([exe, str(stride), "8"] + extra, capture_output=True, text=True, timeout=300)
+        checked, bad = map(int, r.stdout.split())
+        assert checked > 1000000 and bad == 0, (extra, r.stdout, r.stderr[:500])
+
+
 def test_oracle_softcap_known_values():
     """orc_softcap against values fixed by the mathematics: tanh(0) = 0 (sign
     kept), tanh saturates to +-1 at |x| >= 22 (so cap * 1 = cap), tanh(x) ~ x

@@ -71,16 +71,28 @@ def test_noalloc_row_kernel_and_large_k(cuda):
     _same(*_run_pair(w))
 
 
+def test_noalloc_softcap_matches_dlk_sample(cuda):
+    """The soft-cap inside the sampling kernels (no second buffer): C5 rows with
+    cap 30, two calls of decreasing size, equal to dlk_sample's."""
+    from diskllm_amd import api
+    for rows in (24, 8):
+        w = W.c5(rows=rows)
+        _announce(f"noalloc softcap 30 C5 rows={rows}")
+        a, b = api.to_device(w), api.to_device(w)
+        prm = api.params_of(w)
+        prm.softcap = 30.0
+        assert _call("dlk_sample_noalloc", a, prm) == _lib.DLK_OK
+        assert _call("dlk_sample", b, prm) == _lib.DLK_OK
+        _same(api.results(a), api.results(b))
+
+
 def test_noalloc_refuses_what_needs_more(cuda):
     """Calls that would need a second buffer are refused with
-    DLK_ERR_UNSUPPORTED: the soft-cap and histories above 1024 ids."""
+    DLK_ERR_UNSUPPORTED: histories above 1024 ids (their penalties run on a
+    scratch copy of the rows)."""
     from diskllm_amd import api
     w = W.c2(rows=2)
     db = api.to_device(w)
-    prm = api.params_of(w)
-    prm.softcap = 30.0
-    _announce("noalloc refuses softcap")
-    assert _call("dlk_sample_noalloc", db, prm) == _lib.DLK_ERR_UNSUPPORTED
     prm = api.params_of(w, max_history=5000)
     _announce("noalloc refuses max_history 5000")
     assert _call("dlk_sample_noalloc", db, prm) == _lib.DLK_ERR_UNSUPPORTED
