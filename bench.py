@@ -110,19 +110,21 @@ def other_bytes(w) -> int:
 
 
 def run_other(name: str, args) -> int:
-    """One JSON line for workload C1, C3, C4 or C5 (parity-test configurations;
-    the headline line is C2): the step is one dlk_sample call (C4: one
-    dlk_dfa_mask call for its 16 rows), inputs resident in HBM, timed with HIP
-    events on the launch stream."""
+    """One JSON line for workload C1, C3, C4, C5, C5CAP or CAP (parity-test
+    configurations; the headline line is C2): the step is one dlk_sample call
+    (C5/C5CAP: the DFA mask pass, then dlk_sample; C4: one dlk_dfa_mask call for
+    its 16 rows; CAP: the soft-cap epilogue alone), inputs resident in HBM, timed
+    with HIP events on the launch stream."""
     import numpy as np
     import torch
     from diskllm_amd import api, workloads
     from oracle import oracle as O
     dev = torch.device("cuda:0")
     w = workloads.CONFIGS[name]()
+    gpu_ids = None
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    if name == "C5CAP":
+    if name == "CAP":
         from diskllm_amd import _lib
         w.epilogue = True
         cap = workloads.CAP_C5CAP
@@ -184,6 +186,7 @@ def run_other(name: str, args) -> int:
                 api.sample(db, params, sh)
         step()
         res = api.results(db)
+        gpu_ids = res["ids"]
         check = list(range(min(w.rows, 32)))
         orc = O.run_workload(w, check)
         n_ok = int(np.sum(res["ids"][check] == orc["ids"]))
@@ -218,21 +221,25 @@ def run_other(name: str, args) -> int:
                      "ms_per_launch": round(ms_dev, 5)},
         "cpu_baseline": None,
     }
-    if name == "C5CAP":
+    if name == "CAP":
         line["roofline"]["kernel"] = "dlk::softcap_vec_kernel"
-    if w.dfa is not None and name != "C4":
+    if w.dfa is not None and name not in ("C4", "CAP"):
         line["config"]["step"] = ("dlk_dfa_mask over every DFA state (the mask table, rebuilt inside each timed "
-                                  "step), then one dlk_sample call whose rows pick their state's mask row")
+                                  "step), then one dlk_sample call whose rows pick their state's mask row"
+                                  + (f", with softcap {w.softcap:g} applied inside the sampling kernels"
+                                     if w.softcap > 0.0 else ""))
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_other(w, args.cpu_runs)
+        line["cpu_baseline"] = cpu_other(w, args.cpu_runs, gpu_ids)
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_other(w, runs: int) -> dict:
+def cpu_other(w, runs: int, gpu_ids=None) -> dict:
     """CPU time of the same step: C1/C3 the reference src/sampler.c (strict
     build, masks applied as -inf first); C4 the oracle's byte-DFA walk (the DFA
-    mask has no counterpart in the reference); C5 both, on a 32-row sample."""
+    mask has no counterpart in the reference); C5 both, on a 32-row sample;
+    C5CAP the reference's soft-cap loop (host libm tanhf, one thread) in front of
+    C5's."""
     import numpy as np
     from oracle import oracle as O
     nthreads = host_threads()
@@ -262,6 +269,12 @@ def cpu_other(w, runs: int) -> dict:
         return None
     rows = list(range(min(w.rows, 32)))
     lg = np.ascontiguousarray(w.logits[rows])
+    cap_s = 0.0
+    if w.softcap > 0.0:
+        x = lg.reshape(-1)
+        t0 = time.perf_counter()
+        O.lib().orc_softcap(x, x, x.size, np.float32(w.softcap))
+        cap_s = time.perf_counter() - t0
     mask = None
     mw = 0
     dfa_s = 0.0
@@ -295,11 +308,39 @@ def cpu_other(w, runs: int) -> dict:
                            np.ascontiguousarray(w.seeds[rows]), th, runs, ms, ids)
     if rc != 0:
         return None
-    sec = float(np.median(ms)) / 1e3 + dfa_s
-    return {"value": round(len(rows) / sec, 1), "unit": "rows/s", "cores": th,
+    sec = float(np.median(ms)) / 1e3 + dfa_s + cap_s
+    fast_cap = None
+    F = O.ref("fast")
+    if w.softcap > 0.0 and F is not None:
+        # the reference Makefile's -O3 -ffast-math build of the soft-cap loop and of
+        # the sampler on the same rows: bit agreement of the capped logits and of
+        # the token ids with the strict build's
+        raw = np.ascontiguousarray(w.logits[rows])
+        fl = raw.copy()
+        F.refh_softcap(fl.reshape(-1), fl.size, np.float32(w.softcap))
+        same = int(np.count_nonzero(fl.view(np.uint32) == lg.view(np.uint32)))
+        fids = np.zeros(len(rows), np.int32)
+        fms = np.zeros(1, np.float64)
+        rc = F.refh_time_batch(fl, len(rows), w.vocab, hoff.ctypes.data if hoff is not None else None,
+                               hids.ctypes.data if hids is not None else None,
+                               mask.ctypes.data if mask is not None else None, mw, w.order, w.repeat_penalty,
+                               w.frequency_penalty, w.presence_penalty, C.byref(cfg),
+                               np.ascontiguousarray(w.seeds[rows]), th, 1, fms, fids)
+        if rc == 0:
+            fast_cap = {"capped_logits_bit_identical": f"{same}/{fl.size}",
+                        "ids_agree_with_strict": f"{int(np.sum(fids == ids))}/{len(rows)}"}
+    out = {"value": round(len(rows) / sec, 1), "unit": "rows/s", "cores": th,
             "kind": "reference",
             "sample": f"rows 0..{len(rows) - 1}, median of {runs} runs, strict -std=c11 -O2 build"
-                      + ("; DFA mask rows by oracle/oracle.c orc_dfa_mask, one per distinct state" if w.dfa is not None else "")}
+                      + ("; DFA mask rows by oracle/oracle.c orc_dfa_mask, one per distinct state" if w.dfa is not None else "")
+                      + (f"; soft-cap {w.softcap:g} first by oracle/oracle.c orc_softcap (host libm tanhf, one "
+                         f"thread, src/core/context.c:873-876), one pass" if w.softcap > 0.0 else "")}
+    if gpu_ids is not None:
+        # the reference build's ids against the GPU's first-step ids (same seeds)
+        out["ids_match_gpu"] = f"{int(np.sum(ids == np.asarray(gpu_ids)[rows]))}/{len(rows)}"
+    if fast_cap is not None:
+        out["fast_math_build"] = fast_cap
+    return out
 
 
 def main() -> int:
@@ -309,7 +350,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP"],
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP", "CAP"],
                     help="C2 (default) is the headline line; the others are the scope table's parity "
                          "configurations, measured the same way")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

@@ -106,7 +106,7 @@ def params_of(w: Workload, max_history: int = 0, path: int = 0) -> _lib.SamplePa
     if mh <= 0 and w.hist_off is not None and len(w.hist_off) > 1:
         mh = int(np.max(np.diff(w.hist_off)))
     return _lib.SampleParams(w.temperature, w.top_k, w.top_p, w.min_p, w.repeat_penalty, w.frequency_penalty,
-                             w.presence_penalty, w.order, max(mh, 1), w.n_out, path)
+                             w.presence_penalty, w.order, max(mh, 1), w.n_out, path, w.softcap)
 
 
 def batch_struct(db: DeviceBatch) -> _lib.Batch:

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <algorithm>
 #include <vector>
 
 #include "sampler_params.h"
@@ -16,7 +17,8 @@
 #include "sampler_full.h"
 
 extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t lds_bytes, hipStream_t stream);
-extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream);
+extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, size_t lds, hipStream_t stream);
+extern "C" int dlk_topk_kernel_occupancy(int kind, size_t lds);
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap);
 extern "C" int dlk_launch_prepare_rows(const float *src, int64_t ld, float *dst, int64_t dld, int rows, int vocab,
@@ -192,36 +194,63 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     const int T = kTopkThreads;
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     const int k = p.greedy ? 1 : p.top_k;
-    if (k > 1024) return 1;
+    if (k > kTopkMaxK) return 1;
+    if (p.greedy && p.cap > 0.0f) return 1;
     const int KP = k + 16;
-    int ept = 4, G = 0;
-    const int epts[5] = {64, 32, 16, 8, 4};
-    for (int e : epts) {
-        int g = (vocab + e * T - 1) / (e * T);
-        /* the merge keeps 4 words per slice (+2) in a T-word LDS array */
-        if ((int64_t)g * KP > 4096 || 4 * g + 2 > T) break;
-        ept = e;
-        G = g;
-        /* the largest slices that still give one workgroup per CU: more, shorter
-         * workgroups add merge work faster than they add memory parallelism
-         * (32 x 151,936, top-k 50: 8 elements per thread 64 us, 16 or 32 48 us;
-         * 512 x 262,144, top-k 64: 64 per thread 538 us, 32 767 us) */
-        if ((int64_t)rows * g >= 256) break;
+    const int kind = p.cap > 0.0f ? 1 : p.greedy ? 2 : 0;
+    const int unit = 16 * T;                          /* slices are whole batches of 4 groups per thread */
+    const int gmax = std::min(kTopkMaxG, kMergePerThread * T / KP);
+    const int gmin = (vocab + kTopkMaxS - 1) / kTopkMaxS;
+    if (gmin > gmax) return 1;
+    int cc = 512;
+    while (cc < 2 * KP) cc <<= 1;
+    /* LDS of a launch with slices of S: the kernel's carve order -- misc, select
+     * histogram, merge words, then one region for the slice (penalised-group
+     * bits, listed groups, candidates) and the merge (entries, pipeline aggregates;
+     * the fallback's kp entries + 2048-word histogram) */
+    auto lds_for = [&](int S, int G) {
+        const int gc = S / 4 < kTopkGroupCap ? S / 4 : kTopkGroupCap;
+        const size_t slice_b = r16((size_t)(S / 128) * 4) + r16((size_t)gc * 4) + r16((size_t)cc * 8);
+        const size_t merge_b = r16((size_t)cc * 8) + (p.greedy ? 0 : aggs_bytes(k));
+        const size_t fall_b = (size_t)p.plan.kp * 8 + 2048 * 4;
+        size_t work = slice_b > merge_b ? slice_b : merge_b;
+        if (fall_b > work) work = fall_b;
+        return fixed_lds(p.plan) + r16(64 * 4) + r16((size_t)kSelWords * 4) + r16((size_t)(3 * G + 2) * 4) + work;
+    };
+    /* the most workgroups per row that still run as one resident round (each
+     * workgroup's post-stream latency is then paid once), else the fewest */
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
+    static int n_cu[64];
+    if (dev < 0 || dev >= 64) return DLK_ERR_HIP;
+    if (!n_cu[dev] && hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return DLK_ERR_HIP;
+    struct Occ { int dev, kind; size_t lds; int n; };
+    static std::vector<Occ> occ_cache;
+    auto resident = [&](size_t lds) {
+        for (const auto &e : occ_cache)
+            if (e.dev == dev && e.kind == kind && e.lds == lds) return e.n * n_cu[dev];
+        const int n = dlk_topk_kernel_occupancy(kind, lds);
+        occ_cache.push_back(Occ{dev, kind, lds, n});
+        return n * n_cu[dev];
+    };
+    auto slice_of = [&](int g) { return ((vocab + g - 1) / g + unit - 1) / unit * unit; };
+    int S = slice_of(gmin);
+    for (int g = gmax; g >= gmin; g--) {
+        const int s = slice_of(g), gr = (vocab + s - 1) / s;
+        if ((int64_t)rows * gr <= resident(lds_for(s, gr))) { S = s; break; }
     }
-    if (G == 0 || 4 * G + 2 > T) return 1;
+    const int G = (vocab + S - 1) / S;
     TopkParams f;
     memset(&f, 0, sizeof(f));
     f.p = p;
     f.G = G;
-    f.S = ept * T;
+    f.S = S;
     f.KP = KP;
-    int need = G * KP;
-    int bc = 2048;
-    while (bc < need || bc < p.plan.kp + 1024) bc <<= 1;
-    f.buf_cap = bc;
-    size_t lds = fixed_lds(p.plan) + r16((size_t)(f.S / 32) * 4) + r16((size_t)T * 4) + r16(64 * 4) +
-                 r16((size_t)bc * 8) + r16((size_t)kSelWords * 4) + (p.greedy ? 0 : aggs_bytes(k));
-    if (lds > kMaxLds) return 1;
+    f.grp_cap = S / 4 < kTopkGroupCap ? S / 4 : kTopkGroupCap;
+    f.cand_cap = cc;
+    f.buf_cap = cc;
+    const size_t lds = lds_for(S, G);
     size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
     size_t n_cand = (size_t)rows * G * KP * 8;
     WsView ws;
@@ -229,7 +258,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     f.counters = ws.counters;
     f.slots = (TopkSlot *)ws.data;
     f.cands = (uint64_t *)(ws.data + n_slot);
-    return dlk_launch_topk_kernel(&f, rows, ept, lds, stream) == 0 ? DLK_OK : DLK_ERR_HIP;
+    return dlk_launch_topk_kernel(&f, rows, lds, stream) == 0 ? DLK_OK : DLK_ERR_HIP;
 }
 
 /* Fused full-vocabulary path (sampler_full.hip): DLK_OK, or 1 when outside its

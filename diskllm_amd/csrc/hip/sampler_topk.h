@@ -8,9 +8,13 @@
 
 namespace dlk {
 
-constexpr int kTopkThreads = 512;
+constexpr int kTopkThreads = 256;
 constexpr int kSelWords = 260;              /* radix-select histogram (256) + broadcast words */
-constexpr int kMergePerThread = 8;          /* merge: candidates per thread (G * KP <= 4096) */
+constexpr int kMergePerThread = 8;          /* merge: candidates per thread (G * KP <= 2048) */
+constexpr int kTopkGroupCap = 1024;         /* listed 16-byte groups per slice at most (more: the row falls back) */
+constexpr int kTopkMaxG = 64;               /* workgroups per row */
+constexpr int kTopkMaxS = 65536;            /* slice length */
+constexpr int kTopkMaxK = 496;              /* four waves' thresholds need KP = k + 16 <= 4 * 128 */
 
 /* What each slice workgroup publishes (relaxed agent-scope atomic stores). */
 struct TopkSlot {
@@ -27,9 +31,11 @@ struct TopkSlot {
 struct TopkParams {
     RowParams p;
     int G;               /* workgroups per row */
-    int S;               /* slice length = EPT * kTopkThreads */
+    int S;               /* slice length: a multiple of 16 * kTopkThreads, at most kTopkMaxS */
     int KP;              /* candidates kept per slice: min(k + 16, ...) */
-    int buf_cap;         /* LDS collect / merge buffer entries (power of two) */
+    int buf_cap;         /* merge buffer entries (LDS) */
+    int grp_cap;         /* listed groups per slice (LDS) */
+    int cand_cap;        /* slice candidates (LDS) */
     uint32_t *counters;  /* [rows], zero between launches */
     TopkSlot *slots;     /* [rows * G] */
     uint64_t *cands;     /* [rows * G * KP] */

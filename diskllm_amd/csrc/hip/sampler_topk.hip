@@ -59,12 +59,100 @@ DLK_DEV float penalised(const RowParams &p, float x, int cnt) {
 /* Soft-cap (CAP): y = cap * tanhf(x / cap) is non-decreasing in x (tanhf is
  * non-decreasing from float to float: tests/native/tanhf_monotone_check.c), so a
  * slice is streamed and thresholded on its raw logits -- with +-inf clamped to
- * +-FLT_MAX, which the cap maps to the same +-cap -- and only the elements it
+ * +-FLT_MAX, which the cap maps to the same +-cap -- and only the candidates it
  * collects are capped; the penalty patches are capped values, handled from
  * their LDS list.  Ties that the cap creates are resolved by the order
  * (y desc, index asc) of the collected candidates and the merge's certificate. */
-template <int EPT, bool CAP>
-__global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
+
+/* Key of the r-th largest of the 128 ascending keys a, b held two per lane: the
+ * largest K with at least r keys >= K, found bit by bit from ballots (no LDS, no
+ * barrier).  Every lane returns it. */
+DLK_DEV uint32_t wave_rth_key(uint32_t a, uint32_t b, int r) {
+    uint32_t K = 0;
+#pragma unroll
+    for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t c = K | (1u << bit);
+        const int n = __popcll(ballot(a >= c)) + __popcll(ballot(b >= c));
+        if (n >= r) K = c;
+    }
+    return K;
+}
+
+/* The value of an ascending key from wave_rth_key, -inf for keys at or below -inf's. */
+DLK_DEV float asc_value(uint32_t K) { return K > asc_key(-INFINITY) ? key_value(~K) : -INFINITY; }
+
+/* x where bit c of `live` is set, else -inf (a bitfield extract and insert). */
+DLK_DEV float live_or_ninf(float x, uint32_t live, int c) {
+    const int m = (int)(live << (31 - c)) >> 31;
+    return __int_as_float((__float_as_int(x) & m) | ((int)0xff800000 & ~m));
+}
+
+/* The 16-byte group of row elements i0 .. i0 + 3 (i0 a multiple of 4), -inf past s1. */
+DLK_DEV float4 load_group(const float *lg, int i0, int s1) {
+    if (i0 + 3 < s1) return *(const float4 *)(lg + i0);
+    float4 x = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (i0 < s1) x.x = lg[i0];
+    if (i0 + 1 < s1) x.y = lg[i0 + 1];
+    if (i0 + 2 < s1) x.z = lg[i0 + 2];
+    return x;
+}
+
+/* Bits of the group at i0 whose entries come from the stream: inside the slice,
+ * allowed by the mask word bits `mw` (already shifted to i0), not penalised.  A
+ * penalised id sets its group's bit in gbits; such groups look their ids up in
+ * the slice's patch list (pid[0 .. np)). */
+DLK_DEV uint32_t group_live(uint32_t mw, const uint32_t *gbits, const int *pid, int np, int i0, int s0, int s1) {
+    uint32_t live = mw;
+    if (i0 + 4 > s1) live &= i0 < s1 ? (1u << (s1 - i0)) - 1u : 0u;
+    const int gr = (i0 - s0) >> 2;
+    if ((gbits[gr >> 5] >> (gr & 31)) & 1u)
+        for (int k = 0; k < np; k++) {
+            const unsigned d = (unsigned)(pid[k] - i0);
+            if (d < 4u) live &= ~(1u << d);
+        }
+    return live & 0xFu;
+}
+
+/* Whether id (inside the slice) is one of the penalised ids. */
+DLK_DEV bool is_patched(const uint32_t *gbits, const int *pid, int np, int id, int s0) {
+    const int gr = (id - s0) >> 2;
+    if (!((gbits[gr >> 5] >> (gr & 31)) & 1u)) return false;
+    for (int k = 0; k < np; k++)
+        if (pid[k] == id) return true;
+    return false;
+}
+
+/* Bits of the group at i0 allowed by the mask word bits `mw` and inside the slice. */
+DLK_DEV uint32_t range_live(uint32_t mw, int i0, int s1) {
+    uint32_t live = mw;
+    if (i0 + 4 > s1) live &= i0 < s1 ? (1u << (s1 - i0)) - 1u : 0u;
+    return live & 0xFu;
+}
+
+DLK_DEV int lanes_below(uint64_t bal) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+}
+
+/* The slice of a row that one workgroup streams: groups of four elements at
+ * s0 + 4 * (t + j * T), j = 0 .. S/(4T) - 1, in batches of four groups per thread
+ * with the next batch's loads in flight.
+ *   - The penalised ids of the slice are patched from an LDS list (their stream
+ *     entries count as -inf and the list is folded in afterwards).
+ *   - Threshold: after batch 0 each wave takes the ceil(KP/4)-th largest of its
+ *     lanes' two best group maxima (distinct entries, so the wave holds at least
+ *     that many entries at or above it); the smallest of the four is a valid
+ *     bound for the slice's KP-th largest entry.  Refreshed the same way after the
+ *     last batch, from every batch's maxima.
+ *   - Groups whose maximum reaches the threshold are listed in LDS; afterwards
+ *     they are reloaded (from cache) and their entries at or above the final
+ *     threshold become the candidates, of which the first KP under (value desc,
+ *     index asc) are published.
+ *   - Finite counts come from the mask bits; a non-finite raw logit anywhere in
+ *     the slice sends it through an exact recount (NaN / +inf make the row
+ *     irregular, -inf is not finite).
+ * GREEDY keeps only the maximum and its lowest index. */
+template <bool CAP, bool GREEDY>
+__global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
     const int g = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = lane_id(), w = wave_id();
@@ -73,17 +161,37 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     const float *lg = p.logits + (int64_t)row * p.ld;
     const uint32_t *mk = nullptr;
     if (p.mask) mk = p.mask + (int64_t)(p.mask_row ? p.mask_row[row] : row) * p.mask_ld;
+    constexpr int kSpecial = CAP ? (1 | 2) : (1 | 2 | 4 | 512);     /* class bits: NaN (and -inf, +inf) */
 
-    /* LDS: the row-kernel layout (for the in-workgroup fallback) + fast-path buffers */
+    /* LDS: the row-kernel layout (for the in-workgroup fallback), a few words,
+     * then one region the slice and the merge use in turn */
     Lds L = make_lds(smem, p.plan);
     unsigned char *q = L.region;
-    uint32_t *sbits = (uint32_t *)carve(q, (size_t)(f.S / 32) * 4);          /* patched positions in slice */
-    float *tmax = (float *)carve(q, (size_t)T * 4);
     int *misc = (int *)carve(q, 64 * 4);
     int *selh = (int *)carve(q, kSelWords * 4);                           /* radix-select histogram */
-    uint64_t *buf = (uint64_t *)carve(q, (size_t)f.buf_cap * 8);           /* collect / merge / fallback (+ aggs) */
+    uint32_t *sk = (uint32_t *)carve(q, (size_t)(3 * G + 2) * 4);          /* merge: per-slice words, tau */
+    unsigned char *work = q;
+    uint32_t *gbits = (uint32_t *)carve(q, (size_t)(f.S / 128) * 4);       /* slice: groups holding penalised ids */
+    uint32_t *grp = (uint32_t *)carve(q, (size_t)f.grp_cap * 4);           /* slice: listed groups */
+    uint64_t *cbuf = (uint64_t *)carve(q, (size_t)f.cand_cap * 8);         /* slice: candidates */
+    uint64_t *buf = (uint64_t *)work;                                       /* merge: f.buf_cap entries, then aggregates */
     if (t < 32) L.tab[t] = kExp2Tab[t];
     const uint64_t rng0 = p.greedy ? 0ull : p.rng[row];     /* read early: only the merge uses (and writes) it */
+
+    auto gpos = [&](int b, int j) { return s0 + 4 * (t + (4 * b + j) * T); };
+    float4 xa[4];
+    uint32_t ma[4];
+    auto load_batch = [&](float4 (&x)[4], uint32_t (&m)[4], int b) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i0 = gpos(b, j);
+            x[j] = load_group(lg, i0, s1);
+            m[j] = (mk && i0 < s1) ? mk[i0 >> 5] >> (i0 & 31) : 0xFu;
+        }
+    };
+    /* batch 0 first: in flight while the history is read (one register set:
+     * the other resident waves keep loads in flight) */
+    load_batch(xa, ma, 0);
 
     const int32_t *hist = nullptr;
     int nh = 0;
@@ -91,7 +199,6 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         hist = p.hist_ids + p.hist_off[row];
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
-
     if (nh > p.plan.hcap) {
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
@@ -99,172 +206,311 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         }
         return;
     }
-    /* ---- 1. penalty patches of the ids inside this slice ---------------- */
-    for (int i = t; i < f.S / 32; i += T) sbits[i] = 0;
-    if (t == 0) misc[0] = 0;
-    __syncthreads();
-    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
-    for (int i = t; i < nh; i += T) hl[i] = hist[i];
-    __syncthreads();
-    for (int i = t; i < nh; i += T) {             /* in-slice occurrences, first occurrence only */
-        int id = hl[i];
-        if (id < s0 || id >= s1) continue;
-        bool first = true;
-        int cnt = 0;
-        for (int j = 0; j < nh; j++) {
-            int o = hl[j];
-            if (o == id) { cnt++; if (j < i) first = false; }
-        }
-        if (!first) continue;
-        float x = lg[id];
-        if (CAP) x = dlk_softcap_glibc(x, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
-        if (mk && !((mk[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-        x = penalised(p, x, cnt);
-        int at = atomicAdd(&misc[0], 1);
-        if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = x; }
-        atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
-    }
-    __syncthreads();
-    const int np = min(misc[0], p.plan.hcap);
+    int hid = t < nh ? hist[t] : -1;               /* the first T history ids, read early */
+    for (int i = t; i < f.S / 128; i += T) gbits[i] = 0;
+    if (t < 16) misc[t] = 0;                       /* (16.. are written before they are read) */
 
-    /* ---- 2. stream the slice into registers ---------------------------- */
-    float v[EPT];
-    float tm = -INFINITY;
-    int targ = 0x7fffffff, nfin = 0, irr = 0;
-#pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        const int i0 = s0 + 4 * (t + j4 * T);
-        float4 x4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (i0 + 3 < s1) {
-            x4 = *(const float4 *)(lg + i0);
-        } else {
-            if (i0 < s1) x4.x = lg[i0];
-            if (i0 + 1 < s1) x4.y = lg[i0 + 1];
-            if (i0 + 2 < s1) x4.z = lg[i0 + 2];
+    /* penalty patches of the ids inside this slice: misc[0] entries of
+     * (pid, pval), their groups' bits in gbits, misc[11] of them allowed by the mask */
+    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
+    auto build_patches_slice = [&]() {
+        if (t < nh) hl[t] = hid;
+        for (int i = t + T; i < nh; i += T) hl[i] = hist[i];
+        __syncthreads();
+        for (int i = t; i < nh; i += T) {         /* in-slice occurrences, first occurrence only */
+            const int id = hl[i];
+            if (id < s0 || id >= s1) continue;
+            float v = lg[id];                      /* in flight during the count */
+            const uint32_t mword = mk ? mk[id >> 5] : 0xffffffffu;
+            bool first = true;
+            int cnt = 0;
+            for (int j = 0; j < nh; j++) {
+                const int o = hl[j];
+                if (o == id) { cnt++; if (j < i) first = false; }
+            }
+            if (!first) continue;
+            const bool allowed = (mword >> (id & 31)) & 1u;
+            if (CAP) v = dlk_softcap_glibc(v, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
+            if (!allowed) v = -INFINITY;
+            v = penalised(p, v, cnt);
+            const int at = atomicAdd(&misc[0], 1);
+            if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = v; }
+            if (allowed) atomicAdd(&misc[11], 1);
+            atomicOr(&gbits[(id - s0) >> 7], 1u << (((id - s0) >> 2) & 31));
         }
-        float xs[4] = {x4.x, x4.y, x4.z, x4.w};
-        uint32_t mw = 0xffffffffu;
-        if (mk && i0 < s1) mw = mk[i0 >> 5] >> (i0 & 31);
-        uint32_t pb = 0;
-        if (i0 < s1) pb = (sbits[(i0 - s0) >> 5] >> ((i0 - s0) & 31)) & 0xFu;
+        __syncthreads();
+    };
+    if (GREEDY) build_patches_slice();             /* greedy streams exact values */
+    int np = GREEDY ? min(misc[0], p.plan.hcap) : 0;
+
+    /* ---- 2. stream the slice -------------------------------------------- */
+    float m1 = -INFINITY, m2 = -INFINITY;          /* the lane's two best group maxima */
+    int gi = -1;                                   /* GREEDY: first group holding m1 */
+    int nfl = 0;                                   /* stream entries allowed by the mask */
+    uint64_t spc = 0;                              /* ballot: a non-finite raw logit seen */
+    float thr = -INFINITY;
+    const int nb = f.S / (16 * T);                 /* batches of four groups per thread */
+    auto batch = [&](const float4 (&x)[4], const uint32_t (&m)[4], int b) {
+        float gm[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int i = i0 + c;
-            float x = xs[c];
-            if (CAP && !(x != x)) x = fminf(fmaxf(x, -kFltMax), kFltMax);   /* raw stand-in of cap(x) */
-            if (!((mw >> c) & 1u)) x = -INFINITY;
-            if ((pb >> c) & 1u) {
-                if (CAP) {
-                    x = -INFINITY;                 /* a capped patch: from the LDS list below */
-                } else {
-                    for (int k = 0; k < np; k++)
-                        if (L.pid[k] == i) x = L.pval[k];
+        for (int j = 0; j < 4; j++) {
+            const int i0 = gpos(b, j);
+            /* (non-greedy: the penalised ids stream their raw logits; the
+             * patches come after the stream) */
+            const uint32_t live = GREEDY ? group_live(m[j], gbits, L.pid, np, i0, s0, s1) : range_live(m[j], i0, s1);
+            const float4 v = x[j];
+            float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (!GREEDY) spc |= ballot(__builtin_amdgcn_class(e[c], kSpecial));
+                float y = e[c];
+                if (CAP) y = fminf(fmaxf(y, -kFltMax), kFltMax);   /* raw stand-in of cap(x) */
+                e[c] = live_or_ninf(y, live, c);
+            }
+            gm[j] = fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3]));
+            if (GREEDY) {
+                if (gm[j] > m1) { m1 = gm[j]; gi = i0; }
+            } else {
+                nfl += __popc(live);
+                m2 = fmaxf(m2, fminf(m1, gm[j]));
+                m1 = fmaxf(m1, gm[j]);
+            }
+        }
+        if (!GREEDY) {
+            /* the threshold after batches 0, 1, 3, 7, ...: every slot holds a
+             * valid bound at all times (each only grows), so after the first
+             * barrier a wave reads them as they are */
+            if (((b + 1) & b) == 0) {
+                const uint32_t K = wave_rth_key(asc_key(m1), asc_key(m2), (f.KP + 3) / 4);
+                if (lane == 0) misc[16 + w] = (int)K;
+                if (b == 0) __syncthreads();
+                uint32_t Km = (uint32_t)misc[16];
+                for (int u = 1; u < T / 64; u++) Km = min(Km, (uint32_t)misc[16 + u]);
+                thr = asc_value(Km);
+            }
+            const float te = thr > -INFINITY ? thr : -kFltMax;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool take = gm[j] >= te;
+                const uint64_t bal = ballot(take);
+                if (bal) {
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(&misc[1], __popcll(bal));
+                    base = __builtin_amdgcn_readfirstlane(base);
+                    const int at = base + lanes_below(bal);
+                    if (take && at < f.grp_cap) grp[at] = (uint32_t)gpos(b, j);
                 }
             }
-            if (i >= s1) x = -INFINITY;
-            v[j4 * 4 + c] = x;
-            if (i < s1) {
-                if (x > tm || (x == tm && i < targ)) { tm = x; targ = i; }
-                nfin += (x > -INFINITY);
-                irr |= !(x < INFINITY) && !(x == -INFINITY);
-            }
         }
+    };
+#pragma clang loop unroll(disable)
+    for (int b = 0; b < nb; b++) {
+        batch(xa, ma, b);
+        if (b + 1 < nb) load_batch(xa, ma, b + 1);
     }
-    float pmax = -INFINITY;                        /* CAP: largest capped patch */
-    if (CAP) {
-        for (int k = t; k < np; k += T) {
-            const float y = L.pval[k];
-            nfin += y > -INFINITY;
-            irr |= !(y < INFINITY) && !(y == -INFINITY);
+
+    float bm;
+    int bi = 0x7fffffff, nf = 0, irr = 0, kept = 0, complete = 1;
+    uint32_t last_key = 0, fnan = 0;
+    if (GREEDY) {
+        /* ---- 3g. slice maximum and its lowest index --------------------- */
+        if (gi >= 0) {
+            const float4 v = load_group(lg, gi, s1);
+            const uint32_t mwg = mk ? mk[gi >> 5] >> (gi & 31) : 0xFu;
+            const uint32_t live = group_live(mwg, gbits, L.pid, np, gi, s0, s1);
+            const float e[4] = {v.x, v.y, v.z, v.w};
+            for (int c = 3; c >= 0; c--)
+                if (live_or_ninf(e[c], live, c) == m1) bi = gi + c;
+        }
+        bm = m1;
+        for (int k2 = t; k2 < np; k2 += T) {
+            const float y = L.pval[k2];
+            const int id = L.pid[k2];
+            /* (a row whose maximum is -inf samples index 0: no index is taken then) */
+            if (y > bm || (y == bm && y > -INFINITY && id < bi)) { bm = y; bi = id; }
+        }
+        block_argmax(bm, bi, L);
+        if (g == 0 && t == 0) {
+            /* the reference compares from logits[0] (src/sampler.c:10-17): NaN there wins */
+            float x0 = lg[0];
+            if (mk && !(mk[0] & 1u)) x0 = -INFINITY;
+            for (int k2 = 0; k2 < np; k2++)
+                if (L.pid[k2] == 0) x0 = L.pval[k2];
+            fnan = isnan(x0) ? 1u : 0u;
+        }
+    } else {
+        /* ---- 3. patches, finite count; an exact pass when needed -------- */
+        {
+            /* the final threshold, from every batch (read after the patches' barriers) */
+            const uint32_t K = wave_rth_key(asc_key(m1), asc_key(m2), (f.KP + 3) / 4);
+            if (lane == 0) misc[16 + w] = (int)K;
+        }
+        int wn = nfl;
+        for (int m = 32; m >= 1; m >>= 1) wn += shfl_xor(wn, m);
+        if (lane == 0) {
+            atomicAdd(&misc[3], wn);
+            if (spc) misc[8] = 1;
+        }
+        build_patches_slice();
+        np = min(misc[0], p.plan.hcap);
+        float pmax = -INFINITY;
+        int pn = 0, pirr = 0;
+        for (int k2 = t; k2 < np; k2 += T) {       /* the patches: capped values under CAP */
+            const float y = L.pval[k2];
+            pn += y > -INFINITY;
+            pirr |= !(y < INFINITY) && !(y == -INFINITY);
             pmax = fmaxf(pmax, y);
         }
-    }
-    /* ---- 3. workgroup max / argmax / finite count ----------------------- */
-    float bm = tm;
-    int bi = targ;
-    block_argmax(bm, bi, L);
-    int nf = block_sum_int(nfin, L);
-    irr = block_sum_int(irr, L);
-    if (CAP) {
-        /* the slice maximum of the capped row (the argmax serves greedy
-         * sampling, which does not take this path under a cap) */
-        uint32_t pbits = asc_key(pmax);             /* ascending keys: the largest key is the maximum */
-        for (int m2 = 32; m2 >= 1; m2 >>= 1) pbits = max(pbits, (uint32_t)shfl_xor((int)pbits, m2));
-        if (lane == 0) misc[24 + w] = (int)pbits;
+        if (pn) atomicAdd(&misc[4], pn);
+        if (pirr) misc[5] = 1;
+        if (pmax > -INFINITY) atomicMax((unsigned *)&misc[7], asc_key(pmax));
         __syncthreads();
-        for (int u = 0; u < T / 64; u++) pbits = max(pbits, (uint32_t)misc[24 + u]);
-        __syncthreads();
-        const float pm = key_value(~pbits);
-        const float cm = bm > -INFINITY ? dlk_softcap_glibc(bm, p.cap) : bm;
-        bm = fmaxf(cm, pm);
-    }
-    TopkSlot *slot = f.slots + ((int64_t)row * G + g);
-    uint64_t *cands = f.cands + ((int64_t)row * G + g) * f.KP;
-
-    int kept = 0, complete = 1;
-    uint32_t last_key = 0;
-    if (!p.greedy && nf > 0) {
-        /* ---- 4. threshold: the KP-th largest thread maximum ------------- */
-        ((uint32_t *)tmax)[t] = asc_key(tm);
-        __syncthreads();
-        const int KP = f.KP;
-        const uint32_t *tk32 = (const uint32_t *)tmax;
-        const uint32_t thr_key = block_select_u32(T, T - min(KP, T), [&](int i) { return tk32[i]; }, selh, selh + 256);
-        float thr = key_value(~thr_key);
-        if (!(thr > -INFINITY)) thr = -INFINITY;
-        /* CAP: the patches at or above the capped threshold join the candidates */
-        const float cthr = CAP && thr > -INFINITY ? dlk_softcap_glibc(thr, p.cap) : -INFINITY;
-        /* ---- 5. collect finite elements >= thr ------------------------- */
-        /* a count per thread, one block prefix, then the writes */
-        uint32_t cnt = 0;
-#pragma unroll
-        for (int j = 0; j < EPT; j++) cnt += (v[j] > -INFINITY && v[j] >= thr) ? 1u : 0u;
-        if (CAP)
-            for (int k = t; k < np; k += T) cnt += (L.pval[k] > -INFINITY && L.pval[k] >= cthr) ? 1u : 0u;
-        const uint32_t incl = wave_scan_sat_u32(cnt, 0xffffffffu);
-        if (lane == 63) misc[8 + w] = (int)incl;
-        __syncthreads();
-        int at = (int)(incl - cnt), C = 0;
-        for (int u = 0; u < T / 64; u++) {
-            if (u < w) at += misc[8 + u];
-            C += misc[8 + u];
+        nf = misc[3] - misc[11] + misc[4];         /* allowed stream entries, penalised ones replaced */
+        {
+            uint32_t Km = (uint32_t)misc[16];
+            for (int u = 1; u < T / 64; u++) Km = min(Km, (uint32_t)misc[16 + u]);
+            thr = asc_value(Km);
         }
-#pragma unroll
-        for (int j = 0; j < EPT; j++) {
-            const float x = v[j];
-            if (x > -INFINITY && x >= thr) {
-                const float y = CAP ? dlk_softcap_glibc(x, p.cap) : x;
-                if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)(s0 + 4 * (t + (j / 4) * T) + (j & 3));
-                at++;
+        irr = misc[5];
+        const float pmv = asc_value((uint32_t)misc[7]);
+        /* the exact pass (at most once): every group of the slice with the
+         * penalised ids left out -- finite count and irregular entries (under CAP
+         * after the clamp), the stream maximum, and a valid threshold from the
+         * exact group maxima */
+        bool exact_done = false;
+        float smax = -INFINITY, ethr = -INFINITY;
+        auto exact_pass = [&]() {
+            int c2 = 0, ir = 0;
+            float e1 = -INFINITY, e2 = -INFINITY;
+            for (int k2 = t; k2 < f.S / 4; k2 += T) {
+                const int i0 = s0 + 4 * k2;
+                const float4 v = load_group(lg, i0, s1);
+                const uint32_t live =
+                    group_live(mk && i0 < s1 ? mk[i0 >> 5] >> (i0 & 31) : 0xFu, gbits, L.pid, np, i0, s0, s1);
+                const float e[4] = {v.x, v.y, v.z, v.w};
+                float gmx = -INFINITY;
+                for (int c = 0; c < 4; c++) {
+                    if (!((live >> c) & 1u)) continue;
+                    float y = e[c];
+                    if (CAP && !(y != y)) y = fminf(fmaxf(y, -kFltMax), kFltMax);
+                    c2 += y > -INFINITY;
+                    ir |= !(y < INFINITY) && !(y == -INFINITY);
+                    gmx = fmaxf(gmx, y);
+                }
+                e2 = fmaxf(e2, fminf(e1, gmx));
+                e1 = fmaxf(e1, gmx);
             }
-        }
-        if (CAP) {
-            for (int k = t; k < np; k += T) {
-                const float y = L.pval[k];
-                if (y > -INFINITY && y >= cthr) {
-                    if (at < f.buf_cap) buf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)L.pid[k];
-                    at++;
+            float wmx = e1;
+            for (int m = 32; m >= 1; m >>= 1) {
+                c2 += shfl_xor(c2, m);
+                ir |= shfl_xor(ir, m);
+                wmx = fmaxf(wmx, shfl_xor(wmx, m));
+            }
+            const uint32_t K = wave_rth_key(asc_key(e1), asc_key(e2), (f.KP + 3) / 4);
+            if (lane == 0) {
+                atomicAdd(&misc[12], c2);
+                if (ir) misc[13] = 1;
+                atomicMax((unsigned *)&misc[14], asc_key(wmx));
+                misc[16 + w] = (int)K;
+            }
+            __syncthreads();
+            nf = misc[12] + misc[4];
+            irr |= misc[13];
+            smax = asc_value((uint32_t)misc[14]);
+            uint32_t Km = (uint32_t)misc[16];
+            for (int u = 1; u < T / 64; u++) Km = min(Km, (uint32_t)misc[16 + u]);
+            ethr = asc_value(Km);
+            exact_done = true;
+        };
+        if (misc[8]) exact_pass();
+        /* ---- 4. candidates: the entries at or above the threshold -------- */
+        bool all_groups = false, over = false;
+        int C = 0;
+        for (int attempt = 0; attempt < 2; attempt++) {
+            const float te = thr > -INFINITY ? thr : -kFltMax;
+            const float cte = !CAP ? te : thr > -INFINITY ? dlk_softcap_glibc(thr, p.cap) : -INFINITY;
+            const int ng = misc[1];
+            const int lim = all_groups ? f.S / 4 : min(ng, f.grp_cap);
+            for (int k2 = t; k2 < lim; k2 += T) {
+                const int i0 = all_groups ? s0 + 4 * k2 : (int)grp[k2];
+                if (i0 >= s1) continue;
+                const float4 v = load_group(lg, i0, s1);
+                const uint32_t live = group_live(mk ? mk[i0 >> 5] >> (i0 & 31) : 0xFu, gbits, L.pid, np, i0, s0, s1);
+                const float e[4] = {v.x, v.y, v.z, v.w};
+                for (int c = 0; c < 4; c++) {
+                    float y = e[c];
+                    if (CAP) y = fminf(fmaxf(y, -kFltMax), kFltMax);
+                    if (((live >> c) & 1u) && y >= te) {
+                        const int at = atomicAdd(&misc[10], 1);
+                        if (at < f.cand_cap) cbuf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)(i0 + c);
+                    }
                 }
             }
-        }
-        __syncthreads();
-        if (C > f.buf_cap) {
-            complete = -1;                     /* overflow: the merge falls back */
-        } else {
-            int P = 64;
-            while (P < C) P <<= 1;
-            for (int i = C + t; i < P; i += T) buf[i] = ~0ull;
+            for (int k2 = t; k2 < np; k2 += T) {
+                const float y = L.pval[k2];
+                if (y > -INFINITY && y >= cte) {
+                    const int at = atomicAdd(&misc[10], 1);
+                    if (at < f.cand_cap) cbuf[at] = ((uint64_t)desc_key(y) << 32) | (uint32_t)L.pid[k2];
+                }
+            }
             __syncthreads();
-            /* keys carry their index: distinct, so a rank sort when they fit */
-            if (C <= T) rank_sort_distinct(buf, C);
-            else bitonic_sort(buf, P);
-            kept = min(KP, C);
-            complete = (C == nf) ? 1 : 0;
-            last_key = (uint32_t)(buf[kept - 1] >> 32);
-            for (int j = t; j < kept; j += T) pub64(&cands[j], buf[j]);
+            C = misc[10];
+            over = (!all_groups && ng > f.grp_cap) || C > f.cand_cap;
+            if (over && !exact_done) exact_pass();  /* the row falls back: its maximum must be exact */
+            if (over || C >= f.KP || C >= nf) break;
+            /* fewer than KP entries reach a threshold taken from raw logits
+             * (penalties lowered some of them): the exact threshold, every group */
+            if (!exact_done) exact_pass();
+            thr = ethr;
+            all_groups = true;
+            if (t == 0) misc[10] = 0;
+            __syncthreads();
+        }
+        bm = -INFINITY;
+        if (exact_done) {
+            bm = smax;
+            if (CAP && bm > -INFINITY) bm = dlk_softcap_glibc(bm, p.cap);
+            bm = fmaxf(bm, pmv);
+        }
+        if (over) {
+            complete = -1;                         /* overflow: the merge falls back */
+        } else if (C > 0) {
+            if (CAP) {
+                /* cap the streamed entries (the patches' values are capped already) */
+                for (int i = t; i < C; i += T) {
+                    const uint64_t e = cbuf[i];
+                    const uint32_t id = (uint32_t)e;
+                    if (!is_patched(gbits, L.pid, np, (int)id, s0)) {
+                        const float y = dlk_softcap_glibc(key_value((uint32_t)(e >> 32)), p.cap);
+                        cbuf[i] = ((uint64_t)desc_key(y) << 32) | id;
+                    }
+                }
+                __syncthreads();
+            }
+            const int n = C;
+            if (n <= T) {
+                rank_sort_distinct(cbuf, n);
+            } else {
+                int P = 64;
+                while (P < n) P <<= 1;
+                for (int i = n + t; i < P; i += T) cbuf[i] = ~0ull;
+                __syncthreads();
+                bitonic_sort(cbuf, P);
+            }
+            /* every entry at or above the threshold is here, so the first is the
+             * slice maximum */
+            if (!exact_done) bm = key_value((uint32_t)(cbuf[0] >> 32));
+            kept = min(f.KP, n);
+            complete = kept == nf ? 1 : 0;
+            last_key = (uint32_t)(cbuf[kept - 1] >> 32);
+            uint64_t *cands = f.cands + ((int64_t)row * G + g) * f.KP;
+            for (int j = t; j < kept; j += T) pub64(&cands[j], cbuf[j]);
+        } else {
+            complete = nf == 0 ? 1 : 0;
         }
     }
-    /* ---- 6. publish and elect the merging workgroup --------------------- */
+    TopkSlot *slot = f.slots + ((int64_t)row * G + g);
+    /* ---- 5. publish and elect the merging workgroup --------------------- */
     if (t == 0) {
         pub32(&slot->max_bits, f2u(bm));
         pub32(&slot->argmax, (uint32_t)bi);
@@ -272,7 +518,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
         pub32(&slot->kept, (uint32_t)kept);
         pub32(&slot->complete, (uint32_t)complete);
         pub32(&slot->last_key, last_key);
-        pub32(&slot->first_nan, ((g == 0 && isnan(v[0])) ? 1u : 0u) | (irr ? 2u : 0u));
+        pub32(&slot->first_nan, fnan | (irr ? 2u : 0u));
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -284,51 +530,53 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     if (!misc[2]) return;
 
     /* ===================== merge (last workgroup of the row) ============== */
-    if (t == 0) pub32(&f.counters[row], 0u);
-    /* slot h -> LDS (misc[16..]: kept, complete, last_key per slice; up to 64 slices per pass) */
-    uint32_t *sk = (uint32_t *)tmax;                 /* tmax is free now: 3 words per slice */
+    /* one round trip: every slice's words and every candidate slot (slot j of
+     * slice h holds its (j+1)-th best entry when j < kept_h) */
+    const int KP = f.KP, GK = G * KP;
+    const uint64_t *crow = f.cands + (int64_t)row * GK;
+    uint64_t cv[kMergePerThread];
+#pragma unroll
+    for (int u = 0; u < kMergePerThread; u++) {
+        const int i = t + u * T;
+        cv[u] = i < GK ? get64(&crow[i]) : ~0ull;
+    }
+    uint32_t *sw = (uint32_t *)selh;               /* max, argmax, nfin, first_nan per slice (G <= 64) */
+    if (t < G) {
+        const TopkSlot *s = f.slots + ((int64_t)row * G + t);
+        sk[3 * t + 0] = get32(&s->kept);
+        sk[3 * t + 1] = get32(&s->complete);
+        sk[3 * t + 2] = get32(&s->last_key);
+        sw[t] = get32(&s->max_bits);
+        sw[64 + t] = get32(&s->argmax);
+        sw[128 + t] = get32(&s->nfin);
+        sw[192 + t] = get32(&s->first_nan);
+    }
+    uint32_t *tau = sk + 3 * G, *tau2 = sk + 3 * G + 1;
+    if (t == 0) { pub32(&f.counters[row], 0u); *tau = 0xffffffffu; *tau2 = 0u; misc[46] = 0; }
+    __syncthreads();
+    /* every wave reduces the slices itself (the argmax keeps the larger value,
+     * ties to the lower index, as in order) */
     float M = -INFINITY;
     int amax = 0x7fffffff, NF = 0, total = 0, overflow = 0, first_nan = 0, irregular = 0;
-    for (int h = t; h < G; h += T) {
-        TopkSlot *s = f.slots + ((int64_t)row * G + h);
-        sk[3 * h + 0] = get32(&s->kept);
-        sk[3 * h + 1] = get32(&s->complete);
-        sk[3 * h + 2] = get32(&s->last_key);
-        buf[h] = ((uint64_t)get32(&s->max_bits) << 32) | get32(&s->argmax);
-        buf[G + h] = ((uint64_t)get32(&s->nfin) << 32) | get32(&s->first_nan);
+    if (lane < G) {
+        M = u2f(sw[lane]);
+        amax = (int)sw[64 + lane];
+        NF = (int)sw[128 + lane];
+        first_nan = (int)(sw[192 + lane] & 1u);
+        irregular = (int)(sw[192 + lane] & 2u);
+        total = (int)sk[3 * lane];
+        overflow = (int)sk[3 * lane + 1] == -1;
     }
-    __syncthreads();
-    if (w == 0) {
-        /* one wave: slices lane, lane + 64, ...; then lane reductions (the
-         * argmax keeps the larger value, ties to the lower index, as in order) */
-        for (int h = lane; h < G; h += 64) {
-            const float m = u2f((uint32_t)(buf[h] >> 32));
-            const int a = (int)(uint32_t)buf[h];
-            if (m > M || (m == M && a < amax)) { M = m; amax = a; }
-            NF += (int)(buf[G + h] >> 32);
-            first_nan |= (int)((uint32_t)buf[G + h] & 1u);
-            irregular |= (int)((uint32_t)buf[G + h] & 2u);
-            total += (int)sk[3 * h];
-            overflow |= (int)sk[3 * h + 1] == -1;
-        }
-        for (int m2 = 32; m2 >= 1; m2 >>= 1) {
-            const float om = shfl_xor(M, m2);
-            const int oa = shfl_xor(amax, m2);
-            if (om > M || (om == M && oa < amax)) { M = om; amax = oa; }
-            NF += shfl_xor(NF, m2);
-            first_nan |= shfl_xor(first_nan, m2);
-            irregular |= shfl_xor(irregular, m2);
-            total += shfl_xor(total, m2);
-            overflow |= shfl_xor(overflow, m2);
-        }
-        if (lane == 0) {
-            misc[48] = (int)f2u(M); misc[49] = amax; misc[50] = NF; misc[51] = first_nan;
-            misc[52] = irregular; misc[53] = total; misc[54] = overflow;
-        }
+    for (int m2 = 32; m2 >= 1; m2 >>= 1) {
+        const float om = shfl_xor(M, m2);
+        const int oa = shfl_xor(amax, m2);
+        if (om > M || (om == M && oa < amax)) { M = om; amax = oa; }
+        NF += shfl_xor(NF, m2);
+        first_nan |= shfl_xor(first_nan, m2);
+        irregular |= shfl_xor(irregular, m2);
+        total += shfl_xor(total, m2);
+        overflow |= shfl_xor(overflow, m2);
     }
-    __syncthreads();
-    M = u2f((uint32_t)misc[48]); amax = misc[49]; NF = misc[50]; first_nan = misc[51];
-    irregular = misc[52]; total = misc[53]; overflow = misc[54];
     const int n_out = p.n_out;
     auto out_cands_empty = [&](float pr, float lpv, bool ids_idx, int kk) {
         for (int j = t; j < n_out; j += T) {
@@ -345,7 +593,6 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     }
     uint64_t st = xorshift64(rng0);
     const float r = rand_f32_from(st);
-    __syncthreads();
     if (t == 0) p.rng[row] = st;
     const int k = p.top_k;
     if (irregular) {
@@ -367,39 +614,33 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
     R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = 0; R.pflag = L.pflag;
     R.M = M; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
 
-    /* gather candidates re-keyed on s, sorted (s desc, index asc) */
-    bool ok = !overflow && total <= f.buf_cap;
-    int P = 64;
+    /* candidates re-keyed on s, the ones that can be in the top k gathered and
+     * sorted (s desc, index asc) */
+    bool ok = !overflow;
     if (ok) {
-        /* every candidate read at once: thread t takes the slots t + u * T of
-         * the G x KP candidate array (slot j of slice h holds its (j+1)-th best
-         * logit when j < kept_h) */
-        uint32_t *tau = (uint32_t *)(sk + 3 * G);
-        if (t == 0) { *tau = 0xffffffffu; misc[46] = 0; }
-        __syncthreads();
-        const int KP = f.KP, GK = G * KP;
-        const uint64_t *crow = f.cands + (int64_t)row * GK;
-        uint64_t cv[kMergePerThread];
+        /* bounds for the sort: list h is in logit order and s is monotone in
+         * the logit, so at least k entries have s >= the s of any list's k-th
+         * entry (tau), and when every list holds cq = ceil(k / G) entries, at
+         * least G * cq >= k have s >= the smallest s among the lists' cq-th
+         * entries (tau2); anything whose s is below the better bound is not in
+         * the top k */
+        const int cq = (k + G - 1) / G;
+        const bool all_cq = __popcll(ballot(lane < G && (int)sk[3 * lane] >= cq)) == (unsigned)G;
 #pragma unroll
         for (int u = 0; u < kMergePerThread; u++) {
             const int i = t + u * T;
             const int h = i / KP, j = i - h * KP;
-            cv[u] = (i < GK && j < (int)sk[3 * h]) ? get64(&crow[i]) : ~0ull;
-        }
-        /* a bound for the sort: list h is in logit order and s is monotone in
-         * the logit, so at least k entries have s >= the s of its k-th entry;
-         * anything whose s is below the best such bound is not in the top k */
-#pragma unroll
-        for (int u = 0; u < kMergePerThread; u++) {
-            const int i = t + u * T;
-            if (cv[u] != ~0ull) {
+            if (i < GK && j < (int)sk[3 * h]) {
                 cv[u] = ((uint64_t)desc_key((key_value((uint32_t)(cv[u] >> 32)) - M) * R.inv_t) << 32) |
                         (cv[u] & 0xffffffffull);
-                if (i % KP == k - 1) atomicMin(tau, (uint32_t)(cv[u] >> 32));
+                if (j == k - 1) atomicMin(tau, (uint32_t)(cv[u] >> 32));
+                if (j == cq - 1) atomicMax(tau2, (uint32_t)(cv[u] >> 32));
+            } else {
+                cv[u] = ~0ull;
             }
         }
         __syncthreads();
-        const uint32_t tk = *tau;
+        const uint32_t tk = all_cq ? min(*tau, *tau2) : *tau;
 #pragma unroll
         for (int u = 0; u < kMergePerThread; u++) {
             const bool take = cv[u] != ~0ull && (uint32_t)(cv[u] >> 32) <= tk;
@@ -407,57 +648,37 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
             int base = 0;
             if (lane == 0 && bal) base = atomicAdd(&misc[46], __popcll(bal));
             base = shfl(base, 0);
-            if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = cv[u];
+            const int at = base + lanes_below(bal);
+            if (take && at < f.buf_cap) buf[at] = cv[u];
         }
         __syncthreads();
-        int nsort = misc[46];
-        if (nsort > 64 && nsort >= k) {
-            /* only the k best are needed: the k-th smallest s-key by radix
-             * select, then the entries at or below it (k plus any ties) */
-            const uint32_t K = block_select_u32(nsort, k - 1, [&](int i) { return (uint32_t)(buf[i] >> 32); }, selh,
-                                                selh + 256);
-            uint64_t mine[kMergePerThread];
-#pragma unroll
-            for (int u = 0; u < kMergePerThread; u++) {
-                const int i = t + u * T;
-                mine[u] = i < nsort ? buf[i] : ~0ull;
-            }
-            if (t == 0) misc[47] = 0;
-            __syncthreads();
-#pragma unroll
-            for (int u = 0; u < kMergePerThread; u++) {
-                const bool take = (uint32_t)(mine[u] >> 32) <= K && mine[u] != ~0ull;
-                const uint64_t bal = ballot(take);
-                int base = 0;
-                if (lane == 0 && bal) base = atomicAdd(&misc[47], __popcll(bal));
-                base = shfl(base, 0);
-                if (take) buf[base + __popcll(bal & ((1ull << lane) - 1))] = mine[u];
-            }
-            __syncthreads();
-            nsort = misc[47];
-        }
-        while (P < nsort) P <<= 1;
-        for (int i = nsort + t; i < P; i += T) buf[i] = ~0ull;
-        __syncthreads();
-        if (nsort <= T) rank_sort_distinct(buf, nsort);
-        else bitonic_sort(buf, P);
-        if (NF >= k) {
-            /* certify: every slice that kept only part of its finite elements
-             * must have its last kept candidate strictly below the k-th s */
-            const uint32_t kth = (uint32_t)(buf[k - 1] >> 32);
-            if (t == 0) misc[55] = 0;
-            __syncthreads();
-            for (int h = t; h < G; h += T) {
-                if ((int)sk[3 * h + 1] == 1) continue;
-                const float l = key_value(sk[3 * h + 2]);
-                if (!(desc_key((l - M) * R.inv_t) > kth)) misc[55] = 1;
-            }
-            __syncthreads();
-            if (misc[55]) ok = false;
+        const int nsort = misc[46];
+        if (nsort > f.buf_cap) {
+            ok = false;
         } else {
-            /* fewer finite entries than k: all of them plus the first k-NF
-             * entries that are -inf, in index order */
-            if (total != NF) ok = false;
+            if (nsort <= T) {
+                rank_sort_distinct(buf, nsort);
+            } else {
+                int P = 64;
+                while (P < nsort) P <<= 1;
+                for (int i = nsort + t; i < P; i += T) buf[i] = ~0ull;
+                __syncthreads();
+                bitonic_sort(buf, P);
+            }
+            if (NF >= k) {
+                /* certify: every slice that kept only part of its finite
+                 * elements must have its last kept candidate strictly below
+                 * the k-th s (one wave: G <= 64) */
+                const uint32_t kth = (uint32_t)(buf[k - 1] >> 32);
+                bool bad = false;
+                if (lane < G && (int)sk[3 * lane + 1] != 1)
+                    bad = !(desc_key((key_value(sk[3 * lane + 2]) - M) * R.inv_t) > kth);
+                if (ballot(bad)) ok = false;
+            } else {
+                /* fewer finite entries than k: all of them plus the first k-NF
+                 * entries that are -inf, in index order */
+                if (total != NF) ok = false;
+            }
         }
     }
     __syncthreads();
@@ -530,29 +751,37 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkParams f) {
 }  // namespace dlk
 
 namespace {
-template <bool CAP>
-const void *topk_fn(int which) {
-    using namespace dlk;
-    switch (which) {
-        case 0: return (const void *)topk_kernel<4, CAP>;
-        case 1: return (const void *)topk_kernel<8, CAP>;
-        case 2: return (const void *)topk_kernel<16, CAP>;
-        case 3: return (const void *)topk_kernel<32, CAP>;
-        default: return (const void *)topk_kernel<64, CAP>;
-    }
+template <bool CAP, bool GREEDY>
+const void *topk_fn() {
+    return (const void *)dlk::topk_kernel<CAP, GREEDY>;
+}
+
+const void *topk_kind(int kind) {
+    return kind == 1 ? topk_fn<true, false>() : kind == 2 ? topk_fn<false, true>() : topk_fn<false, false>();
 }
 }  // namespace
 
-extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
+/* Workgroups of the top-k kernel of this kind (0 plain, 1 soft-cap, 2 greedy)
+ * resident per CU with `lds` bytes of dynamic LDS. */
+extern "C" int dlk_topk_kernel_occupancy(int kind, size_t lds) {
+    int n = 0;
+    if (hipFuncSetAttribute(topk_kind(kind), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_kind(kind), dlk::kTopkThreads, lds) != hipSuccess)
+        return 0;
+    return n;
+}
+
+extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, size_t lds, hipStream_t stream) {
     using namespace dlk;
-    static int set[2][5] = {{0, 0, 0, 0, 0}, {0, 0, 0, 0, 0}};
-    const int which = ept == 4 ? 0 : ept == 8 ? 1 : ept == 16 ? 2 : ept == 32 ? 3 : ept == 64 ? 4 : -1;
-    const int cap = f->p.cap > 0.0f ? 1 : 0;
-    if (which < 0) return -1;
-    const void *fn = cap ? topk_fn<true>(which) : topk_fn<false>(which);
-    if (!set[cap][which]) {
+    static int set[3] = {0, 0, 0};
+    const int cap = f->p.cap > 0.0f ? 1 : 0, greedy = f->p.greedy ? 1 : 0;
+    if ((cap && greedy) || f->S % (16 * kTopkThreads) != 0) return -1;
+    const int kind = cap ? 1 : greedy ? 2 : 0;
+    const void *fn = topk_kind(kind);
+    if (!set[kind]) {
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
-        set[cap][which] = 1;
+        set[kind] = 1;
     }
     TopkParams fp = *f;
     void *args[] = {&fp};

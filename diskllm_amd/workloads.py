@@ -62,6 +62,7 @@ class Workload:
     dfa: Optional["DFA"] = None              # byte-DFA mask source
     dfa_states: Optional[np.ndarray] = None  # int32 [rows] active state per row
     n_out: int = 0                           # candidate outputs per row
+    softcap: float = 0.0                     # > 0: logits capped, cap * tanhf(l / cap), before the mask
     extra: dict = field(default_factory=dict)
 
     @property
@@ -190,12 +191,25 @@ def c5(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
                     dfa=DFA(off, data, trans), dfa_states=states, n_out=20)
 
 
-def c5cap(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
-    """The reference's decode epilogue on C5's logits: soft-cap cap * tanhf(x / cap)
-    with cap 30 (the Gemma final-logit cap), in place, 512 x 262144 fp32."""
-    return c5(seed, rows, vocab)
-
-
 CAP_C5CAP = 30.0
 
-CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C4": c4, "C5": c5, "C5CAP": c5cap}
+
+def c5cap(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
+    """C5's decode step with the reference's final-logit soft-cap in front:
+    cap * tanhf(l / cap), cap 30 (the Gemma cap), then mask, penalties and sampling
+    as in C5; 512 x 262144 fp32."""
+    w = c5(seed, rows, vocab)
+    w.name = "C5CAP"
+    w.softcap = CAP_C5CAP
+    return w
+
+
+def cap(seed: int = 5, rows: int = 512, vocab: int = 262144) -> Workload:
+    """The reference's decode epilogue alone on C5's logits: soft-cap
+    cap * tanhf(x / cap) with cap 30, in place, 512 x 262144 fp32."""
+    w = c5(seed, rows, vocab)
+    w.name = "CAP"
+    return w
+
+
+CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C4": c4, "C5": c5, "C5CAP": c5cap, "CAP": cap}

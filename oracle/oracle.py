@@ -109,6 +109,7 @@ def ref(kind: str = "strict") -> Optional[C.CDLL]:
                                       C.c_uint32, C.c_float, C.c_float, C.c_float, C.POINTER(SamplerConfig),
                                       _u64p, C.c_int, C.c_int, _f64p, _i32p]
         L.refh_expf_many.argtypes = [_f32p, _f32p, C.c_long]
+        L.refh_softcap.argtypes = [_f32p, C.c_int, C.c_float]
         L.sampler_apply_repetition_penalty.argtypes = [_f32p, C.c_int, _i32p, C.c_int, C.c_float]
         L.sampler_apply_presence_penalty.argtypes = [_f32p, C.c_int, _i32p, C.c_int, C.c_float]
         L.greedy_sample.argtypes = [_f32p, C.c_int]
@@ -162,9 +163,12 @@ def row_mask(w, r: int) -> Optional[np.ndarray]:
 
 
 def prepared_row(w, r: int) -> np.ndarray:
-    """Row r after the mask and the penalties: the logits sampler_sample sees
+    """Row r after the soft-cap (if the workload has one, src/core/context.c:873-876),
+    the mask and the penalties: the logits sampler_sample sees
     (src/core/sampler_api.c:51-61, with the configured penalty order)."""
     row = np.ascontiguousarray(w.logits[r], np.float32).copy()
+    if getattr(w, "softcap", 0.0) > 0.0:
+        lib().orc_softcap(row, row, row.size, np.float32(w.softcap))
     m = row_mask(w, r)
     if m is not None:
         lib().orc_apply_packed_mask(row, row.size, m)

@@ -136,3 +136,12 @@ int refh_time_batch(const float *logits, int rows, int vocab, const int *hist_of
 void refh_expf_many(const float *x, float *y, long n) {
     for (long i = 0; i < n; i++) y[i] = expf(x[i]);
 }
+
+/* The decode step's final-logit soft-cap, in place (src/core/context.c:604-606 and
+ * :873-876; context.c itself needs the whole model runtime to compile, so its
+ * one-line loop is restated here).  Compiled with each build's flags, so the fast
+ * build shows what the reference Makefile's -O3 -ffast-math makes of it
+ * (x * (1/cap) and gcc's vectorised libmvec tanhf). */
+void refh_softcap(float *logits, int n, float cap) {
+    for (int i = 0; i < n; i++) logits[i] = cap * tanhf(logits[i] / cap);
+}
