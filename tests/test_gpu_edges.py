@@ -138,6 +138,26 @@ def test_penalty_orders(cuda, path):
         run_and_check(w, path)
 
 
+@pytest.mark.parametrize("path", PATHS)
+def test_penalties_on_the_top_entries(cuda, path):
+    """History ids that are each row's best logits (5 to 1000 of them), with
+    penalties strong enough to move them below the rest: the top-k kernel takes
+    its threshold from raw logits before the patches, finds fewer than k + 16
+    entries above it and recomputes it from exact values.  Negative presence
+    lifts ids instead; the last case repeats the first under a soft-cap."""
+    V, rows = 120000, 6
+    rng = np.random.default_rng(77)
+    lg = rng.normal(0, 3, size=(rows, V)).astype(np.float32)
+    best = np.argsort(-lg, axis=1, kind="stable")
+    hist = [list(best[r, :n]) for r, n in enumerate([60, 150, 300, 40, 1000, 5])]
+    for rep, freq, pres, cap in ((50.0, 0.0, 0.0, 0.0), (1.0, 0.0, 25.0, 0.0), (1.3, 0.5, -8.0, 0.0),
+                                 (50.0, 0.0, 0.0, 30.0)):
+        w = make(f"toppen-{rep}-{pres}-{cap}", rows, V, seed=5, temperature=0.9, top_k=40, top_p=0.95, rep=rep,
+                 freq=freq, pres=pres, hist=hist, logits=lg.copy(), n_out=8)
+        w.softcap = cap
+        run_and_check(w, path)
+
+
 @pytest.mark.parametrize("path", [0, 1, 2])
 def test_full_vocab_variants(cuda, path):
     """Full-vocabulary sampling at Qwen vocab through the fused kernel (0), the
