@@ -206,11 +206,11 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     while (cc < 2 * KP) cc <<= 1;
     /* LDS of a launch with slices of S: the kernel's carve order -- misc, select
      * histogram, merge words, then one region for the slice (penalised-group
-     * bits, listed groups, candidates) and the merge (entries, pipeline aggregates;
+     * bits, listed groups and their maxima, candidates) and the merge (entries, pipeline aggregates;
      * the fallback's kp entries + 2048-word histogram) */
     auto lds_for = [&](int S, int G) {
         const int gc = S / 4 < kTopkGroupCap ? S / 4 : kTopkGroupCap;
-        const size_t slice_b = r16((size_t)(S / 128) * 4) + r16((size_t)gc * 4) + r16((size_t)cc * 8);
+        const size_t slice_b = r16((size_t)(S / 128) * 4) + 2 * r16((size_t)gc * 4) + r16((size_t)cc * 8);
         const size_t merge_b = r16((size_t)cc * 8) + (p.greedy ? 0 : aggs_bytes(k));
         const size_t fall_b = (size_t)p.plan.kp * 8 + 2048 * 4;
         size_t work = slice_b > merge_b ? slice_b : merge_b;

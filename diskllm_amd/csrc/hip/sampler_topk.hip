@@ -173,6 +173,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     unsigned char *work = q;
     uint32_t *gbits = (uint32_t *)carve(q, (size_t)(f.S / 128) * 4);       /* slice: groups holding penalised ids */
     uint32_t *grp = (uint32_t *)carve(q, (size_t)f.grp_cap * 4);           /* slice: listed groups */
+    float *gmx = (float *)carve(q, (size_t)f.grp_cap * 4);                 /* slice: their maxima */
     uint64_t *cbuf = (uint64_t *)carve(q, (size_t)f.cand_cap * 8);         /* slice: candidates */
     uint64_t *buf = (uint64_t *)work;                                       /* merge: f.buf_cap entries, then aggregates */
     if (t < 32) L.tab[t] = kExp2Tab[t];
@@ -288,17 +289,28 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
                 for (int u = 1; u < T / 64; u++) Km = min(Km, (uint32_t)misc[16 + u]);
                 thr = asc_value(Km);
             }
+            /* list the groups whose maximum reaches the threshold: one LDS
+             * reservation per wave and batch */
             const float te = thr > -INFINITY ? thr : -kFltMax;
+            uint64_t bal[4];
+            int tot = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const bool take = gm[j] >= te;
-                const uint64_t bal = ballot(take);
-                if (bal) {
-                    int base = 0;
-                    if (lane == 0) base = atomicAdd(&misc[1], __popcll(bal));
-                    base = __builtin_amdgcn_readfirstlane(base);
-                    const int at = base + lanes_below(bal);
-                    if (take && at < f.grp_cap) grp[at] = (uint32_t)gpos(b, j);
+                bal[j] = ballot(gm[j] >= te);
+                tot += (int)__popcll(bal[j]);
+            }
+            if (tot) {
+                int base = 0;
+                if (lane == 0) base = atomicAdd(&misc[1], tot);
+                base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int at = base + lanes_below(bal[j]);
+                    if (gm[j] >= te && at < f.grp_cap) {
+                        grp[at] = (uint32_t)gpos(b, j);
+                        gmx[at] = gm[j];
+                    }
+                    base += (int)__popcll(bal[j]);
                 }
             }
         }
@@ -432,6 +444,8 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
             const int ng = misc[1];
             const int lim = all_groups ? f.S / 4 : min(ng, f.grp_cap);
             for (int k2 = t; k2 < lim; k2 += T) {
+                /* (a listed group below the final threshold holds no candidate) */
+                if (!all_groups && !(gmx[k2] >= te)) continue;
                 const int i0 = all_groups ? s0 + 4 * k2 : (int)grp[k2];
                 if (i0 >= s1) continue;
                 const float4 v = load_group(lg, i0, s1);
