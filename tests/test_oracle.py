@@ -279,6 +279,55 @@ def test_fast_build_agreement():
     assert same >= w.rows // 2
 
 
+def _ref_batch_ids(w, rows):
+    """Token ids of the strict reference build on rows of a workload: the
+    reference's penalties (src/sampler.c:21-52, frequency as the harness states
+    it), the mask as -inf, then sampler_sample (oracle/ref_harness.c
+    refh_time_batch, one run)."""
+    L = O.ref("strict")
+    lg = np.ascontiguousarray(w.logits[rows])
+    if w.softcap > 0.0:
+        for r in range(len(rows)):
+            L.refh_softcap(lg[r], w.vocab, np.float32(w.softcap))
+    mask, mw = None, 0
+    if w.mask is not None:
+        mask = np.ascontiguousarray(w.mask[rows])
+    elif w.dfa is not None:
+        tab = {}
+        mask = np.ascontiguousarray(np.stack([tab.setdefault(int(w.dfa_states[r]),
+                                                             O.dfa_mask(w.dfa, int(w.dfa_states[r]), w.vocab))
+                                              for r in rows]))
+    if mask is not None:
+        mw = mask.shape[1]
+    hoff = hids = None
+    if w.hist_off is not None:
+        lists = [w.hist_ids[w.hist_off[r]:w.hist_off[r + 1]] for r in rows]
+        hoff = np.zeros(len(rows) + 1, np.int32)
+        hoff[1:] = np.cumsum([len(x) for x in lists])
+        hids = np.concatenate(lists).astype(np.int32)
+    cfg = O.SamplerConfig(w.temperature, w.top_k, w.top_p, w.min_p, 1)
+    ids = np.zeros(len(rows), np.int32)
+    ms = np.zeros(1, np.float64)
+    rc = L.refh_time_batch(lg, len(rows), w.vocab, hoff.ctypes.data if hoff is not None else None,
+                           hids.ctypes.data if hids is not None else None,
+                           mask.ctypes.data if mask is not None else None, mw, w.order, w.repeat_penalty,
+                           w.frequency_penalty, w.presence_penalty, C.byref(cfg),
+                           np.ascontiguousarray(w.seeds[rows]), min(8, len(rows)), 1, ms, ids)
+    assert rc == 0
+    return ids
+
+
+@needs_ref
+@pytest.mark.parametrize("name,nrows", [("C1", None), ("C2", None), ("C3", None), ("C5", 16), ("C5CAP", 8)])
+def test_configs_full_size_vs_reference(name, nrows):
+    """The oracle equals the strict reference build at the configurations' full
+    shapes: C1, all 64 rows of C2, all 32 rows of C3, and a sample of C5 (DFA
+    masks from the oracle's walk) and C5CAP (the reference's soft-cap loop first)."""
+    w = W.CONFIGS[name]()
+    rows = list(range(w.rows if nrows is None else nrows))
+    np.testing.assert_array_equal(O.run_workload(w, rows)["ids"], _ref_batch_ids(w, rows))
+
+
 # ----------------------------------------------------------------- golden vectors
 
 GOLDEN = os.path.join(ROOT, "tests", "golden", "sampler_small.npz")
