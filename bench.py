@@ -343,6 +343,118 @@ def cpu_other(w, runs: int, gpu_ids=None) -> dict:
     return out
 
 
+def dropin_vocab(V: int, seed: int = 7):
+    """A synthetic vocabulary of JSON-ish token strings in CSR form (no NUL bytes)."""
+    import numpy as np
+    rng = np.random.Generator(np.random.PCG64(seed))
+    alpha = np.frombuffer(b'{}[]":, 0123456789abcdefghijklmnopqrstuvwxyz', np.uint8)
+    lens = np.minimum(rng.geometric(0.3, size=V), 12).astype(np.uint32)
+    off = np.zeros(V + 1, np.uint32)
+    off[1:] = np.cumsum(lens, dtype=np.uint64).astype(np.uint32)
+    data = alpha[rng.integers(0, alpha.size, int(off[-1]))].astype(np.uint8)
+    return off, np.ascontiguousarray(data)
+
+
+def run_dropin(args) -> int:
+    """One token through the drop-in C API in the order the reference's caller uses
+    it (src/core/sampler_api.c:48-73): diskllm_grammar_apply_mask (JSON grammar,
+    buffer reset before each token) -> sampler_apply_presence_penalty ->
+    sampler_apply_repetition_penalty -> sampler_sample -> diskllm_grammar_advance,
+    on row 0 of C2 (host logits, as the reference passes them; a fresh copy of the
+    row before each token, outside the timed part).  Reports tokens/s, the PCIe
+    bytes each token moves (from the copies the drop-ins make) and the strict
+    reference build running the same sequence on one core."""
+    import numpy as np
+    from diskllm_amd import _lib, workloads
+    L = _lib.lib()
+    w = workloads.c2(rows=1)
+    V = w.vocab
+    off, data = dropin_vocab(V)
+    scratch = C.create_string_buffer(256)
+    voc = _lib.CsrVocab(off.ctypes.data, data.ctypes.data, V, C.cast(scratch, C.c_void_p), 256)
+    get = C.cast(L.dlk_csr_token_str, C.c_void_p)
+    hist = np.ascontiguousarray(w.hist_ids[w.hist_off[0]:w.hist_off[1]], np.int32)
+    row0 = np.ascontiguousarray(w.logits[0])
+    pres, rep, eos = 0.5, 1.15, V - 1
+    cfg = _lib.SamplerConfig(1.0, 0, 0.9, 0.0, 12345)
+
+    def run_seq(lib, steps, warm):
+        s = lib.sampler_create(C.byref(cfg))
+        g = lib.diskllm_grammar_init_json()
+        logits = np.empty_like(row0)
+        toks, ts = [], []
+        for i in range(warm + steps):
+            np.copyto(logits, row0)
+            lib.diskllm_grammar_reset(g)
+            t0 = time.perf_counter()
+            lib.diskllm_grammar_apply_mask(g, logits.ctypes.data, V, C.byref(voc), get, eos)
+            lib.sampler_apply_presence_penalty(logits.ctypes.data, V, hist.ctypes.data, hist.size, C.c_float(pres))
+            lib.sampler_apply_repetition_penalty(logits.ctypes.data, V, hist.ctypes.data, hist.size, C.c_float(rep))
+            tok = lib.sampler_sample(s, logits.ctypes.data, V)
+            if tok != eos:
+                piece = L.dlk_csr_token_str(C.byref(voc), tok)
+                if piece:
+                    lib.diskllm_grammar_advance(g, piece)
+            t1 = time.perf_counter()
+            if i >= warm:
+                toks.append(tok)
+                ts.append(t1 - t0)
+        lib.diskllm_grammar_free(g)
+        lib.sampler_free(s)
+        return toks, ts
+
+    toks, ts = run_seq(L, args.steps, args.warmup)
+    med = float(np.median(ts))
+    # bytes over PCIe per token, from the drop-ins' copies (host <-> device)
+    ids = hist[(hist >= 0) & (hist < V)]
+    nd, m = int(np.unique(ids).size), int(ids.size)
+    words = (V + 31) // 32
+    row_b = C.sizeof(_lib.GrammarRow)
+    now = {"apply_mask": row_b + 4 * words + 4, "presence": 2 * 4 * nd + 4 * m + 8,
+           "repetition": 2 * 4 * nd + 4 * m + 8, "sample": 4 * V + 8 + 4 + 4 + 8}
+    before = {"apply_mask": row_b + 2 * 4 * V + 4, "presence": 2 * 4 * V + 4 * hist.size + 8,
+              "repetition": 2 * 4 * V + 4 * hist.size + 8, "sample": 4 * V + 8 + 4 + 4 + 8}
+    line = {
+        "metric": "DROPIN: tokens/sec through the drop-in C API (mask -> presence -> repetition -> sample -> advance), "
+                  "one row, vocab 151936",
+        "value": round(1.0 / med, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(med * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "DROPIN: row 0 of C2 (N(0,2^2) + Zipf bias, 256-id history, presence 0.5, "
+                               "repetition 1.15, T 1.0, top-p 0.9), JSON grammar over a synthetic 151936-token "
+                               "vocabulary (dlk_csr_token_str callback), host logits",
+                   "rows": 1, "vocab": V, "parallelism": "none (1 GPU)",
+                   "step": "median over steps of one token's calls, the logits copy before it excluded"},
+        "pcie": {"bytes_per_token": sum(now.values()), "by_call": now,
+                 "bytes_per_token_full_row_copies": sum(before.values()),
+                 "note": "penalties move the touched ids only (12 bytes per distinct id each way + the history), "
+                         "apply_mask brings back the packed mask, not the row"},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        from oracle import oracle as O
+        R = O.ref("strict")
+        if R is not None:
+            for fn, at in (("sampler_create", [C.c_void_p]), ("sampler_free", [C.c_void_p]),
+                           ("sampler_sample", [C.c_void_p, C.c_void_p, C.c_int]),
+                           ("sampler_apply_presence_penalty", [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_float]),
+                           ("sampler_apply_repetition_penalty", [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_float]),
+                           ("diskllm_grammar_apply_mask", [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                                           C.c_int])):
+                getattr(R, fn).argtypes = at
+            R.sampler_create.restype = C.c_void_p
+            rtoks, rts = run_seq(R, min(args.steps, 50), args.warmup)   # the same rng steps as ours
+            rmed = float(np.median(rts))
+            same = sum(int(a == b) for a, b in zip(toks, rtoks))
+            line["parity"] = f"{same}/{len(rtoks)} tokens identical to the strict reference build's sequence"
+            line["cpu_baseline"] = {"value": round(1.0 / rmed, 1), "unit": "tokens/s", "cores": 1, "kind": "reference",
+                                    "sample": f"the same sequence through the strict reference build "
+                                              f"(src/core/grammar.c, src/sampler.c), median of {len(rts)} tokens"}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -350,7 +462,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP", "CAP"],
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP", "CAP", "DROPIN"],
                     help="C2 (default) is the headline line; the others are the scope table's parity "
                          "configurations, measured the same way")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -377,6 +489,8 @@ def main() -> int:
     from oracle import oracle as O
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.config == "DROPIN":
+        return run_dropin(args)
     if args.config != "C2":
         return run_other(args.config, args)
     dev = torch.device("cuda:0")

@@ -67,12 +67,18 @@ class GrammarRow(C.Structure):
     _fields_ = [("scan", ScanState), ("bal", BalanceState)]
 
 
+class CsrVocab(C.Structure):
+    """dlk_csr_vocab (include/diskllm_amd.h)."""
+    _fields_ = [("off", C.c_void_p), ("bytes", C.c_void_p), ("vocab", C.c_int), ("scratch", C.c_void_p),
+                ("scratch_cap", C.c_int)]
+
+
 # Every symbol the public headers declare (checked by the CPU test suite).
 EXPORTS = [
     # include/diskllm_amd.h
     "dlk_seed_state", "dlk_sample", "dlk_sample_noalloc", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
     "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
-    "dlk_vocab_csr_from_gguf", "dlk_softcap",
+    "dlk_vocab_csr_from_gguf", "dlk_csr_token_str", "dlk_softcap",
     # include/sampler.h
     "sampler_create", "sampler_free", "sampler_apply_repetition_penalty", "sampler_apply_presence_penalty",
     "sampler_sample", "greedy_sample",
@@ -158,6 +164,8 @@ def lib() -> C.CDLL:
         L.diskllm_grammar_advance.argtypes = [C.c_void_p, C.c_char_p]
         L.diskllm_grammar_is_finished.restype = C.c_bool
         L.diskllm_grammar_is_finished.argtypes = [C.c_void_p]
+        L.dlk_csr_token_str.restype = C.c_char_p
+        L.dlk_csr_token_str.argtypes = [C.c_void_p, C.c_int]
         L.diskllm_grammar_apply_mask.restype = C.c_int
         L.diskllm_grammar_apply_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         _LIB = L

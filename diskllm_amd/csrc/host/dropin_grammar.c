@@ -3,7 +3,9 @@
  * reference's text buffer (src/core/grammar.c:8-14) and the validator state
  * after it; apply_mask rebuilds the token-string table through the caller's
  * callback (as the reference reads it on every call), uploads it only when it
- * changed, and masks every token on the device from the buffer's state.
+ * changed, and masks every token on the device from the buffer's state; only the
+ * packed mask comes back (one bit per token), and the disallowed logits are set
+ * to -inf from it in place.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <math.h>
@@ -31,6 +33,8 @@ struct diskllm_grammar {
     size_t d_bytes_cap;
     int d_vocab_cap;
     dlk_grammar_row *d_row;
+    uint32_t *hmask;             /* host copy of the last mask */
+    int hmask_cap;
     dlk_dropin_ctx dev;
     int dev_ready;
 };
@@ -81,6 +85,7 @@ void diskllm_grammar_free(diskllm_grammar *g) {
     }
     free(g->off);
     free(g->bytes);
+    free(g->hmask);
     free(g);
 }
 
@@ -187,15 +192,31 @@ int diskllm_grammar_apply_mask(diskllm_grammar *g, float *logits, int vocab_size
             hipMemcpyAsync(g->d_bytes, g->bytes, g->tab_bytes, hipMemcpyHostToDevice, st) != hipSuccess)
             return -1;
     }
-    const size_t lbytes = (size_t)vocab_size * sizeof(float);
+    const int words = (vocab_size + 31) / 32;
+    if (words > g->hmask_cap) {
+        uint32_t *nm = realloc(g->hmask, (size_t)words * sizeof(uint32_t));
+        if (!nm) return -1;
+        g->hmask = nm;
+        g->hmask_cap = words;
+    }
     if (hipMemcpyAsync(g->d_row, &g->row, sizeof(g->row), hipMemcpyHostToDevice, st) != hipSuccess) return -1;
-    if (hipMemcpyAsync(g->dev.logits, logits, lbytes, hipMemcpyHostToDevice, st) != hipSuccess) return -1;
     if (dlk_grammar_mask(g->d_off, g->d_bytes, vocab_size, g->d_row, 1, eos_token_id, g->dev.mask, g->dev.mask_cap,
-                         g->dev.logits, vocab_size, g->dev.ids, st) != DLK_OK)
+                         NULL, 0, g->dev.ids, st) != DLK_OK)
         return -1;
     int32_t valid = 0;
-    if (hipMemcpyAsync(logits, g->dev.logits, lbytes, hipMemcpyDeviceToHost, st) != hipSuccess) return -1;
+    if (hipMemcpyAsync(g->hmask, g->dev.mask, (size_t)words * sizeof(uint32_t), hipMemcpyDeviceToHost, st) !=
+        hipSuccess)
+        return -1;
     if (hipMemcpyAsync(&valid, g->dev.ids, sizeof(int32_t), hipMemcpyDeviceToHost, st) != hipSuccess) return -1;
     if (hipStreamSynchronize(st) != hipSuccess) return -1;
+    /* the mask's cleared bits: logits[t] = -INFINITY (src/core/grammar.c:295-305) */
+    for (int w = 0; w < words; w++) {
+        uint32_t off = ~g->hmask[w];
+        while (off) {
+            const int t = 32 * w + __builtin_ctz(off);
+            off &= off - 1u;
+            if (t < vocab_size) logits[t] = -INFINITY;
+        }
+    }
     return valid;
 }

@@ -90,26 +90,64 @@ int greedy_sample(const float *logits, int vocab_size) {
     return id;
 }
 
-/* One penalty op in place on the host row (ids outside [0, vocab) are skipped
- * on the device, as the reference skips them). */
+/* One penalty op in place on the host row.  Only the touched entries cross
+ * PCIe: the logits of the distinct in-range ids (ids outside [0, vocab) are
+ * skipped, as the reference skips them) go up as a compact row, the history as
+ * slots of that row, the device applies the op there, and the compact row comes
+ * back to be written over those ids: 12 bytes per id each way in place of the
+ * whole row.  The order of a history does not matter to either op: repetition
+ * scales an entry once per occurrence (its sign never changes), presence
+ * subtracts once per distinct id. */
+typedef struct { int32_t id, pos; } id_pos;
+
+static int cmp_id_pos(const void *a, const void *b) {
+    const id_pos *x = (const id_pos *)a, *y = (const id_pos *)b;
+    if (x->id != y->id) return x->id < y->id ? -1 : 1;
+    return x->pos < y->pos ? -1 : x->pos > y->pos;
+}
+
 static void penalty_one(float *logits, int vocab, const int *seen, int n, uint32_t op, float value) {
-    dlk_dropin_ctx *c = dlk_dropin_shared_lock();
-    if (!c) return;
-    if (dlk_dropin_reserve(c, vocab, n) == 0) {
-        const int32_t hoff[2] = {0, n};
-        const size_t bytes = (size_t)vocab * sizeof(float);
-        int ok = hipMemcpyAsync(c->logits, logits, bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-                 hipMemcpyAsync(c->hist, seen, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream) ==
-                     hipSuccess &&
-                 hipMemcpyAsync(c->hoff, hoff, sizeof(hoff), hipMemcpyHostToDevice, c->stream) == hipSuccess;
-        if (ok)
-            ok = dlk_apply_penalties(c->logits, vocab, 1, vocab, c->hoff, c->hist, op,
-                                     op == DLK_OP_REPETITION ? value : 1.0f, 0.0f,
-                                     op == DLK_OP_PRESENCE ? value : 0.0f, c->stream) == DLK_OK;
-        if (ok) hipMemcpyAsync(logits, c->logits, bytes, hipMemcpyDeviceToHost, c->stream);
-        hipStreamSynchronize(c->stream);
+    id_pos *ip = malloc((size_t)n * sizeof(id_pos));
+    int32_t *slots = malloc((size_t)n * sizeof(int32_t));
+    int32_t *ids = malloc((size_t)n * sizeof(int32_t));
+    float *vals = malloc((size_t)n * sizeof(float));
+    int m = 0, nd = 0;
+    if (ip && slots && ids && vals) {
+        for (int i = 0; i < n; i++)
+            if (seen[i] >= 0 && seen[i] < vocab) ip[m++] = (id_pos){seen[i], i};
+        qsort(ip, (size_t)m, sizeof(id_pos), cmp_id_pos);
+        for (int j = 0; j < m; j++) {
+            if (j == 0 || ip[j].id != ip[j - 1].id) {
+                ids[nd] = ip[j].id;
+                vals[nd] = logits[ip[j].id];
+                nd++;
+            }
+            slots[j] = nd - 1;
+        }
     }
-    dlk_dropin_shared_unlock();
+    dlk_dropin_ctx *c = nd ? dlk_dropin_shared_lock() : NULL;
+    if (c) {
+        if (dlk_dropin_reserve(c, nd, m) == 0) {
+            const int32_t hoff[2] = {0, m};
+            const size_t bytes = (size_t)nd * sizeof(float);
+            int ok = hipMemcpyAsync(c->logits, vals, bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+                     hipMemcpyAsync(c->hist, slots, (size_t)m * sizeof(int32_t), hipMemcpyHostToDevice,
+                                    c->stream) == hipSuccess &&
+                     hipMemcpyAsync(c->hoff, hoff, sizeof(hoff), hipMemcpyHostToDevice, c->stream) == hipSuccess;
+            if (ok)
+                ok = dlk_apply_penalties(c->logits, nd, 1, nd, c->hoff, c->hist, op,
+                                         op == DLK_OP_REPETITION ? value : 1.0f, 0.0f,
+                                         op == DLK_OP_PRESENCE ? value : 0.0f, c->stream) == DLK_OK;
+            if (ok) ok = hipMemcpyAsync(vals, c->logits, bytes, hipMemcpyDeviceToHost, c->stream) == hipSuccess;
+            if (hipStreamSynchronize(c->stream) == hipSuccess && ok)
+                for (int d = 0; d < nd; d++) logits[ids[d]] = vals[d];
+        }
+        dlk_dropin_shared_unlock();
+    }
+    free(ip);
+    free(slots);
+    free(ids);
+    free(vals);
 }
 
 void sampler_apply_repetition_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,

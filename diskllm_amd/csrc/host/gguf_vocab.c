@@ -148,3 +148,13 @@ int dlk_vocab_csr_from_gguf(const char *path, int vocab, uint32_t *off, uint8_t 
     if (n_bytes) *n_bytes = (int64_t)total;
     return DLK_OK;
 }
+
+const char *dlk_csr_token_str(void *ctx, int token_id) {
+    const dlk_csr_vocab *v = (const dlk_csr_vocab *)ctx;
+    if (!v || !v->off || !v->scratch || v->scratch_cap <= 0 || token_id < 0 || token_id >= v->vocab) return NULL;
+    size_t n = (size_t)(v->off[token_id + 1] - v->off[token_id]);
+    if (n > (size_t)v->scratch_cap - 1) n = (size_t)v->scratch_cap - 1;
+    memcpy(v->scratch, v->bytes + v->off[token_id], n);
+    v->scratch[n] = '\0';
+    return v->scratch;
+}

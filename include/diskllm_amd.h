@@ -227,6 +227,23 @@ int dlk_softcap(float *logits, int64_t ld, int rows, int vocab, float cap, hipSt
 int dlk_vocab_csr_from_gguf(const char *path, int vocab, uint32_t *off, uint8_t *bytes, int64_t bytes_cap,
                             int32_t *n_tokens, int64_t *n_bytes);
 
+/* The token-string callback of diskllm_grammar_apply_mask (include/grammar.h,
+ * src/core/grammar.c:275-308: NUL-terminated strings, NULL for no string) over a
+ * table in the form above, for callers that hold the vocabulary as that table
+ * rather than as a tokenizer (no counterpart in the reference, whose caller
+ * passes tokenizer_decode_raw, src/core/sampler_api.c:42-46).  ctx points to a
+ * dlk_csr_vocab; the string is copied into its scratch buffer (scratch_cap
+ * bytes; longer entries are cut there), so one ctx serves one thread at a time.
+ * NULL for ids outside [0, vocab). */
+typedef struct {
+    const uint32_t *off;      /* [vocab+1] */
+    const uint8_t *bytes;
+    int vocab;
+    char *scratch;            /* [scratch_cap] */
+    int scratch_cap;
+} dlk_csr_vocab;
+const char *dlk_csr_token_str(void *ctx, int token_id);
+
 #ifdef __cplusplus
 }
 #endif

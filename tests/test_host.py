@@ -49,6 +49,23 @@ def test_seed_state():
     assert L.dlk_seed_state(7) == 7
 
 
+def test_csr_token_str():
+    """dlk_csr_token_str: the entry as a NUL-terminated string, NULL outside
+    [0, vocab) or without a scratch buffer, long entries cut at scratch_cap - 1."""
+    L = _lib.lib()
+    toks = [b"ab", b"", b"{\"x\":", b"0123456789"]
+    off = np.zeros(len(toks) + 1, np.uint32)
+    off[1:] = np.cumsum([len(x) for x in toks])
+    data = np.frombuffer(b"".join(toks), np.uint8).copy()
+    scratch = C.create_string_buffer(8)
+    v = _lib.CsrVocab(off.ctypes.data, data.ctypes.data, len(toks), C.cast(scratch, C.c_void_p), 8)
+    assert [L.dlk_csr_token_str(C.byref(v), i) for i in range(3)] == toks[:3]
+    assert L.dlk_csr_token_str(C.byref(v), 3) == b"0123456"
+    assert L.dlk_csr_token_str(C.byref(v), -1) is None and L.dlk_csr_token_str(C.byref(v), 4) is None
+    v.scratch_cap = 0
+    assert L.dlk_csr_token_str(C.byref(v), 0) is None
+
+
 def test_grammar_modes():
     L = _lib.lib()
     assert L.dlk_grammar_mode_of(b'root ::= "{" "\\"bbox_2d\\":" ...') == _lib.GRAMMAR_RECEIPT
