@@ -36,14 +36,26 @@ def fused_kernel_name(rows: int, vocab: int) -> str:
     G = min(16, max(1, (256 + rows - 1) // rows))
     ept = (vocab + G * 1024 - 1) // (G * 1024)
     ept = next(e for e in (16, 24, 32, 40, 48) if ept <= e or e == 48)
-    return f"dlk::full_kernel<{ept}>"
+    return f"dlk::full_kernel<{ept}, false>"
 
 
-def profiled_traffic(kernel: str):
+# The dominant kernel of each workload and its committed traffic summary.
+DOMINANT = {"C1": ("dlk::topk_kernel<false, false>", None),
+            "C3": ("dlk::topk_kernel<false, false>", "topk_kernel_c3"),
+            "C4": ("dlk::dfa_mask_kernel", None),
+            "C5": ("dlk::topk_kernel<false, false>", "topk_kernel_c5"),
+            "C5CAP": ("dlk::topk_kernel<true, false>", None),
+            "CAP": ("dlk::softcap_vec_kernel", "softcap_vec_kernel_cap")}
+
+
+def profiled_traffic(kernel: str, tag: str = "full_kernel_c2"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy of known size), or None
-    when the summary is absent or was taken on another kernel."""
-    path = os.path.join(ROOT, "profiles", "full_kernel_c2_hbm_traffic.txt")
+    profiles/<tag>_hbm_traffic.txt (FETCH_SIZE and WRITE_SIZE passes scaled by a
+    copy of known size), or None when the summary is absent or was taken on
+    another kernel."""
+    if tag is None:
+        return None
+    path = os.path.join(ROOT, "profiles", f"{tag}_hbm_traffic.txt")
     try:
         text = open(path).read()
     except OSError:
@@ -130,8 +142,10 @@ def run_other(name: str, args) -> int:
         cap = workloads.CAP_C5CAP
         lg = api._dev(np.ascontiguousarray(w.logits), dev)
 
-        def step():
+        def step(ev=None):
+            if ev: ev[0].record(stream)
             _lib.check(_lib.lib().dlk_softcap(lg.data_ptr(), w.vocab, w.rows, w.vocab, cap, sh), "dlk_softcap")
+            if ev: ev[1].record(stream)
         step()
         torch.cuda.synchronize()
         got = lg.cpu().numpy()
@@ -151,11 +165,13 @@ def run_other(name: str, args) -> int:
         out = torch.empty((w.rows, W), dtype=torch.int32, device=dev)
         from diskllm_amd import _lib
 
-        def step():
+        def step(ev=None):
+            if ev: ev[0].record(stream)
             rc = _lib.lib().dlk_dfa_mask(t_off.data_ptr(), t_dat.data_ptr(), w.vocab, t_tr.data_ptr(), d.trans.shape[0],
                                          t_st.data_ptr(), w.rows, d.eos_id, d.accept & 0xFFFFFFFFFFFFFFFF,
                                          out.data_ptr(), W, sh)
             _lib.check(rc, "dlk_dfa_mask")
+            if ev: ev[1].record(stream)
         step()
         torch.cuda.synchronize()
         got = out.cpu().numpy().view(np.uint32)
@@ -176,14 +192,18 @@ def run_other(name: str, args) -> int:
             t_all = api._dev(np.arange(n_st, dtype=np.int32), dev)
             W = db.mask.shape[1]
 
-            def step():
+            def step(ev=None):
                 _lib.check(_lib.lib().dlk_dfa_mask(t_off.data_ptr(), t_dat.data_ptr(), w.vocab, t_tr.data_ptr(), n_st,
                                                    t_all.data_ptr(), n_st, d.eos_id, d.accept & 0xFFFFFFFFFFFFFFFF,
                                                    db.mask.data_ptr(), W, sh), "dlk_dfa_mask")
+                if ev: ev[0].record(stream)
                 api.sample(db, params, sh)
+                if ev: ev[1].record(stream)
         else:
-            def step():
+            def step(ev=None):
+                if ev: ev[0].record(stream)
                 api.sample(db, params, sh)
+                if ev: ev[1].record(stream)
         step()
         res = api.results(db)
         gpu_ids = res["ids"]
@@ -194,19 +214,18 @@ def run_other(name: str, args) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+    # HIP events on the launch stream around the dominant kernel's launch of each step
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
+    for k in range(args.steps):
+        step(evs[k])
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
-    ms_dev = ev0.elapsed_time(ev1) / args.steps
+    ms_dev = sum(a.elapsed_time(b) for a, b in evs) / args.steps
     nbytes = other_bytes(w)
     achieved = nbytes / (ms_dev * 1e-3) / 1e9
+    kname, ktag = DOMINANT[name]
     line = {
         "metric": f"{name}: rows/sec + achieved HBM GB/s (% of peak), batch {w.rows}, vocab {w.vocab}",
         "value": round(w.rows / (ms_step * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
@@ -217,12 +236,10 @@ def run_other(name: str, args) -> int:
                    "parallelism": "none (1 GPU)"},
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": nbytes,
-                     "ms_per_launch": round(ms_dev, 5)},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(kname, ktag),
+                     "bytes_per_launch": nbytes, "ms_per_launch": round(ms_dev, 5), "kernel": kname},
         "cpu_baseline": None,
     }
-    if name == "CAP":
-        line["roofline"]["kernel"] = "dlk::softcap_vec_kernel"
     if w.dfa is not None and name not in ("C4", "CAP"):
         line["config"]["step"] = ("dlk_dfa_mask over every DFA state (the mask table, rebuilt inside each timed "
                                   "step), then one dlk_sample call whose rows pick their state's mask row"

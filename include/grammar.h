@@ -4,7 +4,9 @@
  * libdiskllm_amd.so.  The grammar keeps the reference's 8 KiB text buffer and,
  * beside it, the validator state after the buffer (dlk_grammar_row in
  * diskllm_amd.h), updated as tokens are appended, so that apply_mask resumes
- * every token from that state on the GPU instead of rescanning the buffer.
+ * every token from that state on the GPU instead of rescanning the buffer; only
+ * the packed mask (a bit per token) comes back, and the disallowed logits are
+ * set to -inf in place from it.
  */
 #ifndef DISKLLM_GRAMMAR_H
 #define DISKLLM_GRAMMAR_H

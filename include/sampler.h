@@ -1,9 +1,10 @@
 /*
  * sampler.h -- drop-in for DiskLLM's include/sampler.h (same types, names and
  * signatures; include/sampler.h:7-34 of the reference), implemented by
- * libdiskllm_amd.so on the GPU: every call copies the caller's host row to the
- * device, runs the batched kernels of diskllm_amd.h on one row and copies the
- * result back.  Results are bit-identical to the reference built as strict ISO C.
+ * libdiskllm_amd.so on the GPU: sampler_sample copies the caller's host row to
+ * the device and runs the batched kernels of diskllm_amd.h on it; the penalty
+ * functions send only the logits of the history's ids and write them back.
+ * Results are bit-identical to the reference built as strict ISO C.
  *
  * Each sampler owns a HIP stream and device buffers (its own kernel workspace
  * too), so separate samplers may be used from separate threads at once; one
