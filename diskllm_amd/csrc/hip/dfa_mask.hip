@@ -14,7 +14,15 @@
 namespace dlk {
 
 constexpr int kDfaRowsPerBlock = 16;
+constexpr int kDfaRegBytes = 16;          /* token bytes held in registers; longer tokens read the rest */
 
+/* One thread per token and a group of 16 rows per block (grid.y: the row
+ * groups, so that enough waves hide the lookups' latency).  The rows are
+ * stepped together: at each byte position every row takes one table lookup
+ * (independent of the other rows'), so a step is 16 LDS reads in flight rather
+ * than one dependent chain per row.  The table is staged with state 0's row all
+ * zeros and every entry outside the table mapped to 0, so a rejected walk stays
+ * at 0 by itself; the walk ends when no row of any lane of the wave is alive. */
 __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restrict__ off,
                                                        const uint8_t *__restrict__ bytes, int V,
                                                        const uint8_t *__restrict__ trans, int n_states,
@@ -23,35 +31,70 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
     extern __shared__ uint8_t tt[];
     const int n_tt = n_states * 256;
     for (int i = threadIdx.x * 4; i < n_tt; i += blockDim.x * 4) {
-        *(uint32_t *)(tt + i) = *(const uint32_t *)(trans + i);
+        uint32_t w = i < 256 ? 0u : *(const uint32_t *)(trans + i);
+        if (n_states < 256)
+            for (int k = 0; k < 4; k++)
+                if (((w >> (8 * k)) & 255u) >= (uint32_t)n_states) w &= ~(255u << (8 * k));
+        *(uint32_t *)(tt + i) = w;
     }
-    __syncthreads();
     const int tok = blockIdx.x * blockDim.x + threadIdx.x;
     const int lane = lane_id();
     const int W = (V + 31) >> 5;
-    uint32_t b0 = 0, b1 = 0;
-    if (tok < V) { b0 = off[tok]; b1 = off[tok + 1]; }
-    const int r0 = blockIdx.y * kDfaRowsPerBlock;
-    const int r1 = min(n_rows, r0 + kDfaRowsPerBlock);
-    for (int r = r0; r < r1; r++) {
-        const int s0 = states[r];
-        bool ok = false;
-        if (tok < V) {
-            if (tok == eos_id) {
-                ok = s0 > 0 && s0 < 64 && ((accept >> s0) & 1ull);
-            } else {
-                int s = s0;
-                ok = s > 0 && s < n_states && b1 > b0;
-                for (uint32_t j = b0; ok && j < b1; j++) {
-                    s = tt[s * 256 + bytes[j]];
-                    ok = s != 0 && s < n_states;
-                }
+    uint32_t b0 = 0, len = 0;
+    if (tok < V) {
+        b0 = off[tok];
+        len = off[tok + 1] - b0;
+    }
+    /* the token's first bytes, every load issued at once */
+    uint32_t by[kDfaRegBytes];
+#pragma unroll
+    for (int j = 0; j < kDfaRegBytes; j++) by[j] = (uint32_t)j < len ? bytes[b0 + j] : 0u;
+    const bool walk = tok < V && tok != eos_id && len > 0;
+    /* steps every lane of the wave may need: the wave's longest token, up to kDfaRegBytes */
+    uint32_t wl = len < (uint32_t)kDfaRegBytes ? len : (uint32_t)kDfaRegBytes;
+    for (int m = 32; m >= 1; m >>= 1) wl = max(wl, (uint32_t)shfl_xor((int)wl, m));
+    const int wbase = (tok - lane) >> 5;          /* first word of this wave's 64 tokens */
+    __syncthreads();
+    {
+        const int r0 = blockIdx.y * kDfaRowsPerBlock;
+        const int nr = min(n_rows - r0, kDfaRowsPerBlock);
+        uint32_t st[kDfaRowsPerBlock];
+#pragma unroll
+        for (int r = 0; r < kDfaRowsPerBlock; r++) {
+            const int s0 = r < nr ? states[r0 + r] : 0;
+            st[r] = walk && s0 > 0 && s0 < n_states ? (uint32_t)s0 : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kDfaRegBytes; j++) {
+            uint32_t any = 0;
+#pragma unroll
+            for (int r = 0; r < kDfaRowsPerBlock; r++) any |= st[r];
+            if ((uint32_t)j >= wl || !ballot(any != 0u && (uint32_t)j < len)) break;
+            const bool act = (uint32_t)j < len;
+#pragma unroll
+            for (int r = 0; r < kDfaRowsPerBlock; r++) {
+                const uint32_t nx = tt[st[r] * 256u + by[j]];
+                st[r] = act ? nx : st[r];
             }
         }
-        uint64_t bal = ballot(ok);
-        const int wbase = (tok - lane) >> 5;          /* first word of this wave's 64 tokens */
-        if (lane == 0 && wbase < W) out[(int64_t)r * ld + wbase] = (uint32_t)bal;
-        if (lane == 32 && wbase + 1 < W) out[(int64_t)r * ld + wbase + 1] = (uint32_t)(bal >> 32);
+        for (uint32_t j = kDfaRegBytes; j < len; j++) {     /* the rest of a long token */
+            const uint32_t b = bytes[b0 + j];
+#pragma unroll
+            for (int r = 0; r < kDfaRowsPerBlock; r++) st[r] = tt[st[r] * 256u + b];
+        }
+#pragma unroll
+        for (int r = 0; r < kDfaRowsPerBlock; r++) {
+            if (r >= nr) break;
+            bool ok = st[r] != 0u;
+            if (tok == eos_id) {
+                const int s0 = states[r0 + r];
+                ok = s0 > 0 && s0 < 64 && ((accept >> s0) & 1ull);
+            }
+            ok = ok && tok < V;
+            const uint64_t bal = ballot(ok);
+            if (lane == 0 && wbase < W) out[(int64_t)(r0 + r) * ld + wbase] = (uint32_t)bal;
+            if (lane == 32 && wbase + 1 < W) out[(int64_t)(r0 + r) * ld + wbase + 1] = (uint32_t)(bal >> 32);
+        }
     }
 }
 
