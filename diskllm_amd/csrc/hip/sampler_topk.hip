@@ -133,6 +133,42 @@ DLK_DEV int lanes_below(uint64_t bal) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
 }
 
+/* Of the n <= blockDim.x <= 256 entries of buf (sort keys: high word first),
+ * moves those whose high word is at or below the r-th smallest high word (r <= n)
+ * to the front and returns their count (r, plus any ties): the r-th high word
+ * by a bitwise search on one wave, four keys a lane.  slot: two LDS words. */
+DLK_DEV int keep_best(uint64_t *buf, int n, int r, int *slot) {
+    const int t = threadIdx.x, lane = lane_id();
+    const uint64_t mine = t < n ? buf[t] : ~0ull;
+    if (wave_id() == 0) {
+        uint32_t kk[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int i = lane + 64 * q;
+            kk[q] = i < n ? (uint32_t)(buf[i] >> 32) : 0xffffffffu;
+        }
+        uint32_t K = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t c = K | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) cnt += (int)__popcll(ballot(kk[q] < c));
+            if (cnt < r) K = c;
+        }
+        if (lane == 0) { slot[0] = (int)K; slot[1] = 0; }
+    }
+    __syncthreads();
+    const uint32_t Ks = (uint32_t)slot[0];
+    const bool keep = t < n && (uint32_t)(mine >> 32) <= Ks;
+    const uint64_t bk = ballot(keep);
+    int b2 = 0;
+    if (lane == 0 && bk) b2 = atomicAdd(&slot[1], (int)__popcll(bk));
+    b2 = shfl(b2, 0);
+    if (keep) buf[b2 + lanes_below(bk)] = mine;
+    __syncthreads();
+    return slot[1];
+}
+
 /* The slice of a row that one workgroup streams: groups of four elements at
  * s0 + 4 * (t + j * T), j = 0 .. S/(4T) - 1, in batches of four groups per thread
  * with the next batch's loads in flight.
@@ -208,6 +244,14 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         return;
     }
     int hid = t < nh ? hist[t] : -1;               /* the first T history ids, read early */
+    /* and, for those inside the slice, their logit and mask word (in flight
+     * during the stream) */
+    float hval = 0.0f;
+    uint32_t hmw = 0xffffffffu;
+    if (hid >= s0 && hid < s1) {
+        hval = lg[hid];
+        if (mk) hmw = mk[hid >> 5];
+    }
     for (int i = t; i < f.S / 128; i += T) gbits[i] = 0;
     if (t < 16) misc[t] = 0;                       /* (16.. are written before they are read) */
 
@@ -221,8 +265,8 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         for (int i = t; i < nh; i += T) {         /* in-slice occurrences, first occurrence only */
             const int id = hl[i];
             if (id < s0 || id >= s1) continue;
-            float v = lg[id];                      /* in flight during the count */
-            const uint32_t mword = mk ? mk[id >> 5] : 0xffffffffu;
+            float v = i == t ? hval : lg[id];      /* entries past the first T: in flight during the count */
+            const uint32_t mword = i == t ? hmw : (mk ? mk[id >> 5] : 0xffffffffu);
             bool first = true;
             int cnt = 0;
             for (int j = 0; j < nh; j++) {
@@ -501,7 +545,9 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
                 }
                 __syncthreads();
             }
-            const int n = C;
+            int n = C;
+            /* only the KP best are sorted (KP, plus any ties at the KP-th key) */
+            if (n > f.KP + 16 && n <= T) n = keep_best(cbuf, n, f.KP, &misc[20]);
             if (n <= T) {
                 rank_sort_distinct(cbuf, n);
             } else {
@@ -655,21 +701,30 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         }
         __syncthreads();
         const uint32_t tk = all_cq ? min(*tau, *tau2) : *tau;
+        /* the survivors to LDS: one reservation per wave */
+        uint64_t balu[kMergePerThread];
+        int tot = 0;
 #pragma unroll
         for (int u = 0; u < kMergePerThread; u++) {
-            const bool take = cv[u] != ~0ull && (uint32_t)(cv[u] >> 32) <= tk;
-            const uint64_t bal = ballot(take);
-            int base = 0;
-            if (lane == 0 && bal) base = atomicAdd(&misc[46], __popcll(bal));
-            base = shfl(base, 0);
-            const int at = base + lanes_below(bal);
-            if (take && at < f.buf_cap) buf[at] = cv[u];
+            balu[u] = ballot(cv[u] != ~0ull && (uint32_t)(cv[u] >> 32) <= tk);
+            tot += (int)__popcll(balu[u]);
+        }
+        int base = 0;
+        if (lane == 0 && tot) base = atomicAdd(&misc[46], tot);
+        base = shfl(base, 0);
+#pragma unroll
+        for (int u = 0; u < kMergePerThread; u++) {
+            const int at = base + lanes_below(balu[u]);
+            if (((balu[u] >> lane) & 1ull) && at < f.buf_cap) buf[at] = cv[u];
+            base += (int)__popcll(balu[u]);
         }
         __syncthreads();
-        const int nsort = misc[46];
+        int nsort = misc[46];
         if (nsort > f.buf_cap) {
             ok = false;
         } else {
+            /* only the k best are sorted (k, plus any ties at the k-th s-key) */
+            if (nsort > k + 16 && nsort <= T) nsort = keep_best(buf, nsort, k, &misc[48]);
             if (nsort <= T) {
                 rank_sort_distinct(buf, nsort);
             } else {
