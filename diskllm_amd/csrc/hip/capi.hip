@@ -266,7 +266,9 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
 int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStream_t stream) {
     using namespace dlk;
     const int T = kFullThreads;
-    if (p.greedy || p.topk_on || p.minp_on || p.s_general) return 1;
+    if (p.greedy || p.topk_on || p.s_general) return 1;
+    /* min-p with the cut after the first kept entry (it may lie in any slice): the row kernel */
+    if (p.minp_on && p.topp_on && p.top_p <= 0.0f) return 1;
     if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     if (vocab < 8192 || (vocab & 3) != 0) return 1;   /* whole 16-byte groups per row */

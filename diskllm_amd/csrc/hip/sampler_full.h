@@ -24,7 +24,10 @@ enum : int {
 enum : int {
     kPubMax = 0,       /* float bits of the slice maximum */
     kPubE = 1,         /* double: slice sum of e */
-    kPubP = 2,         /* double: slice sum of p */
+    kPubP = 2,         /* double: slice sum of p (min-p: of the kept p * inv2) */
+    kPubS2 = 3,        /* min-p: double, slice sum of the surviving p */
+    kPubA2 = 4,        /* min-p: double, slice sum of every p */
+    kPubN2 = 5,        /* min-p: surviving entries in the slice */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
     kPubF = 9,         /* double: the slice's predicted contribution to the draw's float sum */
     kPubX = 10         /* from the slice holding the top-p crossing: x (bits 0-30, 0x7fffffff: not

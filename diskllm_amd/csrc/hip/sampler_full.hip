@@ -448,6 +448,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     int x = V - 1;
     const bool topp = p.topp_on;
     double RWg = 0.0;                              /* exact-bounded p prefix before this slice */
+    float pk = inv;                                /* prefix of the values at chunk c ~ pk * ce[c] */
     if (ok) {
         /* ---- p and the slice's p total (double, any order) ------------------ */
 #pragma unroll
@@ -462,6 +463,65 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                     if (p.out_cand_probs) p.out_cand_probs[o] = v[j];
                 }
             }
+        }
+        if (p.minp_on) {
+            /* ---- B2: min-p (src/sampler.c:188-202): the entries with p >= min_p
+             *      survive, in index order (none: every entry stays); their
+             *      double sum, certified as inv is, gives inv2.  v becomes
+             *      p * inv2 for the entries kept and 0 for the others (a 0 moves
+             *      neither the top-p sum nor the draw's), and ce the chunk prefix
+             *      of v ------------------------------------------------------ */
+            double s_sv = 0.0, s_all = 0.0;
+            int n_sv = 0;
+#pragma unroll
+            for (int j = 0; j < EPT; j++) {
+                const double d = (double)v[j];
+                s_all += d;
+                if (v[j] >= p.min_p) { s_sv += d; n_sv++; }
+            }
+            s_sv = wave_incl_scan_d(s_sv);
+            s_all = wave_incl_scan_d(s_all);
+            for (int m = 32; m >= 1; m >>= 1) n_sv += shfl_xor(n_sv, m);
+            if (t == 0) misc[12] = 0;
+            if (lane == 63) { L.red[wave_id()] = s_sv; L.red[32 + wave_id()] = s_all; }
+            __syncthreads();
+            if (lane == 0 && n_sv) atomicAdd(&misc[12], n_sv);
+            __syncthreads();
+            if (t == 0) {
+                double a = 0.0, b = 0.0;
+                for (int w2 = 0; w2 < T / 64; w2++) { a += L.red[w2]; b += L.red[32 + w2]; }
+                at_st64(&mypub[kPubS2], d2u(a) | kReady);
+                at_st64(&mypub[kPubA2], d2u(b) | kReady);
+                at_st64(&mypub[kPubN2], (uint64_t)(uint32_t)misc[12] | kReady);
+            }
+            {
+                const int idx[3] = {kPubS2, kPubA2, kPubN2};
+                row_gather(pubrow, G, idx, pc, p.status);
+            }
+            double S2 = 0.0, SA = 0.0;
+            int64_t nkeep = 0;
+            for (int h = 0; h < G; h++) {
+                S2 += u2d(pc[h * kPubWords + kPubS2]);
+                SA += u2d(pc[h * kPubWords + kPubA2]);
+                nkeep += (int64_t)(uint32_t)pc[h * kPubWords + kPubN2];
+            }
+            const bool keep_all = nkeep == 0;
+            const double Sx = keep_all ? SA : S2;
+            const float i2a = (float)(1.0 / (Sx * (1.0 + eps_s)));
+            const float i2b = (float)(1.0 / (Sx * (1.0 - eps_s)));
+            if (i2a != i2b) ok = false;
+            const float inv2 = i2a;
+#pragma unroll
+            for (int j = 0; j < EPT; j++) v[j] = keep_all || v[j] >= p.min_p ? v[j] * inv2 : 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < EPT / 4; j4++) {
+                const float d = (v[4 * j4] + v[4 * j4 + 1]) + (v[4 * j4 + 2] + v[4 * j4 + 3]);
+                const float fs = row_scan_f(d);
+                if ((lane & 15) == 15) ce[(t + j4 * T) >> 4] = (double)fs;
+            }
+            __syncthreads();
+            block_excl_scan(ce, nch, L.red);
+            pk = 1.0f;
         }
         {
             double ps = 0.0;
@@ -527,8 +587,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             __syncthreads();
             for (int c = t; c < nch; c += T) {
                 if (s0 + 64 * c >= s1) continue;
-                const double lo = RWg + (double)inv * ce[c] * (1.0 - dl);
-                const double hi = RWg + (double)inv * ce[c + 1] * (1.0 + dl);
+                const double lo = RWg + (double)pk * ce[c] * (1.0 - dl);
+                const double hi = RWg + (double)pk * ce[c + 1] * (1.0 + dl);
                 if (lo <= tau && tau <= hi) {
                     const int sl = atomicAdd(&misc[1], 1);
                     if (sl < kCandSlots) misc[2 + sl] = c;
@@ -649,7 +709,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     {
         /* p prefix at x: bounded by the prefix at the end of x's chunk */
         int cx = (x - s0) >> 6;
-        Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + (double)inv * ce[min(nch, cx + 1)]);
+        Rx = (x < s0) ? RWg : (x >= s1 ? 1e300 : RWg + (double)pk * ce[min(nch, cx + 1)]);
     }
     /* each chunk's predicted binade: that of its start value when it and its
      * end value, widened by a margin far beyond the float sum's accumulated
@@ -658,10 +718,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      * the double prefix, so certainly by the float sum) */
     const double mu = 0x1p-12;
     for (int c = t; c <= nch; c += T) {
-        const double a = fmin(RWg + (double)inv * ce[c], Rx) * scale;
+        const double a = fmin(RWg + (double)pk * ce[c], Rx) * scale;
         Pc[c] = a;
         if (c < nch) {
-            const double b = fmin(RWg + (double)inv * ce[c + 1], Rx) * scale;
+            const double b = fmin(RWg + (double)pk * ce[c + 1], Rx) * scale;
             const bool zero = ce[c + 1] == ce[c] || s0 + 64 * c > x;
             const int bh = predict_binade<24>(a * (1.0 - mu));
             const bool valid = bh == predict_binade<24>(b * (1.0 + mu)) && bh >= -100;

@@ -41,7 +41,9 @@ def run_and_check(w, path):
                          want_p=w.n_out)
         assert int(res["ids"][r]) == o["token"], (w.name, r, int(res["ids"][r]), o["token"])
         assert int(res["states"][r]) == o["state"], (w.name, r)
-        if w.n_out and o["k"] and not o["greedy"] and np.all(np.isfinite(o["cand_p"])):
+        # (candidate outputs are the softmax stage's entries in buffer order; the
+        # oracle's trace is the buffer after min-p's compaction)
+        if w.n_out and w.min_p == 0.0 and o["k"] and not o["greedy"] and np.all(np.isfinite(o["cand_p"])):
             n = min(w.n_out, o["k"])
             np.testing.assert_array_equal(res["cand_ids"][r, :n], o["cand_idx"][:n])
             np.testing.assert_allclose(res["cand_probs"][r, :n], o["cand_p"][:n], rtol=1e-5)
@@ -156,6 +158,36 @@ def test_penalties_on_the_top_entries(cuda, path):
                  freq=freq, pres=pres, hist=hist, logits=lg.copy(), n_out=8)
         w.softcap = cap
         run_and_check(w, path)
+
+
+@pytest.mark.parametrize("path", [0, 1, 2])
+def test_full_vocab_min_p(cuda, path):
+    """Min-p without top-k at Qwen vocab through the fused kernel (0), the row
+    kernel (1) and the fused kernel's exact fallback (2): survivors p >= min_p in
+    index order, renormalised (src/sampler.c:188-202), then top-p and the draw;
+    min_p 0.5 leaves no survivor, so every entry stays (:195)."""
+    V = 151936
+    for (T, tp, mp, sd) in [(1.0, 0.9, 1e-6, 51), (1.0, 1.0, 1e-5, 52), (0.7, 0.95, 1e-4, 53), (1.3, 0.9, 0.01, 54),
+                            (1.0, 0.9, 0.5, 55), (0.5, 1.0, 0.5, 56)]:
+        w = W.c2(seed=sd, rows=8, vocab=V)
+        w.temperature, w.top_p, w.min_p = T, tp, mp
+        w.n_out = 16
+        res = run_and_check(w, path)
+        if path != 1:
+            # the candidate outputs (softmax stage, buffer order, final log-probabilities)
+            # equal the row kernel's
+            ref = run_and_check(w, 1)
+            for key in ("cand_ids", "cand_probs", "cand_logprobs"):
+                np.testing.assert_array_equal(res[key].view(np.uint32), ref[key].view(np.uint32), err_msg=key)
+    w = W.c2(seed=57, rows=4, vocab=V)
+    w.min_p = 2e-5
+    m = np.zeros((4, (V + 31) // 32), np.uint32)
+    rng = np.random.default_rng(57)
+    for r in range(4):
+        al = rng.choice(V, [3, 1000, 50000, V][r], replace=False)
+        np.bitwise_or.at(m[r], al >> 5, (np.uint32(1) << (al & 31).astype(np.uint32)))
+    w.mask = m
+    run_and_check(w, path)
 
 
 @pytest.mark.parametrize("path", [0, 1, 2])
