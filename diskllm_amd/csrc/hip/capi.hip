@@ -263,7 +263,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
 
 /* Fused full-vocabulary path (sampler_full.hip): DLK_OK, or 1 when outside its
  * range (the caller then uses the row kernel). */
-int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStream_t stream) {
+int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_wait, hipStream_t stream) {
     using namespace dlk;
     const int T = kFullThreads;
     if (p.greedy || p.topk_on || p.s_general) return 1;
@@ -288,6 +288,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, hipStre
     f.S = S;
     f.stage_cap = 64;
     f.force_exact = force_exact;
+    f.spin_limit = no_wait ? 0u : kFullSpinLimit;
     /* carve order of full_kernel: sbits, spre, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
      * tab, tbase, rres, rbase, pc, misc, md */
     const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
@@ -445,8 +446,10 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
         int rc = launch_topk(p, rows, vocab, stream);
         if (rc <= 0) return rc;
     }
-    if ((prm->path == DLK_PATH_AUTO || prm->path == DLK_PATH_FULL_EXACT) && !p.greedy && !p.topk_on) {
-        int rc = launch_full(p, rows, vocab, prm->path == DLK_PATH_FULL_EXACT, stream);
+    if ((prm->path == DLK_PATH_AUTO || prm->path == DLK_PATH_FULL_EXACT || prm->path == DLK_PATH_FULL_NO_WAIT) &&
+        !p.greedy && !p.topk_on) {
+        int rc = launch_full(p, rows, vocab, prm->path == DLK_PATH_FULL_EXACT, prm->path == DLK_PATH_FULL_NO_WAIT,
+                             stream);
         if (rc <= 0) return rc;
     }
     if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;

@@ -13,6 +13,7 @@ constexpr int kFullMaxG = 16;        /* workgroups per row */
 constexpr int kPubWords = 16;        /* 64-bit words each workgroup publishes */
 constexpr int kCandSlots = 2;        /* predicted top-p crossing chunks per workgroup */
 constexpr int kSyncWords = 64;       /* per-row synchronisation words */
+constexpr uint32_t kFullSpinLimit = 1u << 22;   /* polls before a cross-workgroup wait gives up: a few seconds */
 
 /* per-row sync words (all zero between launches) */
 enum : int {
@@ -51,6 +52,9 @@ struct FullParams {
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;
     int force_exact;   /* test hook: send every row through the exact fallback */
+    uint32_t spin_limit;   /* polls after the first before a wait gives up: kFullSpinLimit; 0 (test
+                              hook) makes every wait give up at its first poll that finds a word
+                              not yet written, which sets DLK_STATUS_SYNC_TIMEOUT */
 };
 
 }  // namespace dlk

@@ -35,8 +35,6 @@
 
 namespace dlk {
 
-constexpr uint32_t kSpinLimit = 1u << 22;   /* bounded waits: a few seconds at most */
-
 DLK_DEV void at_st32(uint32_t *a, uint32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DLK_DEV void at_st64(uint64_t *a, uint64_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DLK_DEV uint32_t at_ld32(const uint32_t *a) {
@@ -77,7 +75,7 @@ constexpr uint64_t kReady = 1ull << 63;
  * workgroup.  Wave 0 polls, a word per lane; the wait is bounded. */
 template <int K>
 __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const int (&idx)[K], uint64_t *pc,
-                                           uint32_t *status) {
+                                           uint32_t *status, uint32_t spin_limit) {
     if (wave_id() == 0) {
         const int lane = lane_id(), n = G * K;
         for (int b = 0; b < n; b += 64) {
@@ -89,7 +87,7 @@ __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const 
             while (true) {
                 if (act && !(w & kReady)) w = at_ld64(&pubrow[off]);
                 if (ballot(act && !(w & kReady)) == 0) break;
-                if (++spins > kSpinLimit) {
+                if (++spins > spin_limit) {
                     if (lane == 0 && status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
                     break;
                 }
@@ -388,7 +386,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     {
         const int idx[1] = {kPubMax};
-        row_gather(pubrow, G, idx, pc, p.status);
+        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
     }
     float M = -INFINITY;
     bool row_bad = false;
@@ -432,7 +430,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     /* ---- B: softmax normaliser ------------------------------------------ */
     {
         const int idx[1] = {kPubE};
-        row_gather(pubrow, G, idx, pc, p.status);
+        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
     }
     double Sapx = 0.0;
     for (int h = 0; h < G; h++) Sapx += u2d(pc[h * kPubWords + kPubE]);
@@ -496,7 +494,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             }
             {
                 const int idx[3] = {kPubS2, kPubA2, kPubN2};
-                row_gather(pubrow, G, idx, pc, p.status);
+                row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
             }
             double S2 = 0.0, SA = 0.0;
             int64_t nkeep = 0;
@@ -544,7 +542,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
          *      and certifies them and hands them to the others ----------------- */
         {
             const int idx[2] = {kPubP, kPubP0};
-            row_gather(pubrow, G, idx, pc, p.status);
+            row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
         }
         for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
         const double U = 0x1p-53;
@@ -667,7 +665,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 uint32_t spins = 0;
                 const uint64_t *src = &pubrow[hx * kPubWords + kPubX];
                 while (!((wv = at_ld64(src)) & kReady)) {
-                    if (++spins > kSpinLimit) {
+                    if (++spins > f.spin_limit) {
                         if (lane == 0 && p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
                         wv = kReady | 0x7fffffffull;
                         break;
@@ -859,7 +857,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      *      exact start value (exact for slice 0: the sum starts at 0) ------- */
     {
         const int idx[1] = {kPubF};
-        row_gather(pubrow, G, idx, pc, p.status);
+        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
     }
     double Phat = 0.0;
     for (int h = 0; h < g; h++) Phat += u2d(pc[h * kPubWords + kPubF]);

@@ -68,6 +68,9 @@ typedef struct {
 #define DLK_PATH_AUTO 0        /* fastest path that covers the configuration */
 #define DLK_PATH_ROW 1         /* one workgroup per row, every sum emulated exactly */
 #define DLK_PATH_FULL_EXACT 2  /* fused full-vocabulary kernel with every row finished by its exact fallback */
+#define DLK_PATH_FULL_NO_WAIT 3  /* fused full-vocabulary kernel whose cross-workgroup waits give up at the
+                                   first poll that finds a word not yet written: forces the
+                                   DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid) */
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */

@@ -238,3 +238,34 @@ def test_nan_and_inf_rows(cuda, path):
         w = make(f"nan-inf-k{k}-p{tp}-mp{mp}", rows, V, seed=5, temperature=1.0, top_k=k, top_p=tp, min_p=mp,
                  logits=lg, n_out=12)
         run_and_check(w, path)
+
+
+def test_sync_timeout_path(cuda):
+    """The fused kernel's bounded cross-workgroup waits, made to give up at their
+    first poll that finds a word not yet written (DLK_PATH_FULL_NO_WAIT, set from
+    the host; every launch still runs to its end): the call completes, sets
+    DLK_STATUS_SYNC_TIMEOUT and writes ids inside the vocabulary.  The timed-out
+    launch returns the row's published words to zero like any other, so the next
+    ordinary call on the same stream and workspace is exact again."""
+    from diskllm_amd import _lib, api
+    w = W.c2(rows=16)
+    db = api.to_device(w)
+    ref = [O.sample_row(O.prepared_row(w, r), int(w.seeds[r]), w.temperature, w.top_k, w.top_p, w.min_p)
+           for r in range(w.rows)]
+    for cycle in range(2):
+        print(f"[case] no-wait launch, cycle {cycle}", flush=True)
+        db.reset_rng()
+        db.status.zero_()
+        api.sample(db, api.params_of(w, path=_lib.PATH_FULL_NO_WAIT))
+        res = api.results(db)
+        assert res["status"] & 2, "no wait gave up"
+        assert np.all((res["ids"] >= 0) & (res["ids"] < w.vocab)), res["ids"]
+        print(f"[case] ordinary launch after it, cycle {cycle}", flush=True)
+        db.reset_rng()
+        db.status.zero_()
+        api.sample(db, api.params_of(w))
+        res = api.results(db)
+        assert res["status"] == 0
+        for r in range(w.rows):
+            assert int(res["ids"][r]) == ref[r]["token"], (cycle, r)
+            assert int(res["states"][r]) == ref[r]["state"], (cycle, r)
