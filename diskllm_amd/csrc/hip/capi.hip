@@ -195,6 +195,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     const int k = p.greedy ? 1 : p.top_k;
     if (k > kTopkMaxK) return 1;
+    if (p.plan.hcap > kTopkHcapMax) return 1;     /* (the host stages longer histories elsewhere) */
     if (p.greedy && p.cap > 0.0f) return 1;
     const int KP = k + 16;
     const int kind = p.cap > 0.0f ? 1 : p.greedy ? 2 : 0;

@@ -15,6 +15,7 @@ constexpr int kTopkGroupCap = 1024;         /* listed 16-byte groups per slice a
 constexpr int kTopkMaxG = 64;               /* workgroups per row */
 constexpr int kTopkMaxS = 65536;            /* slice length */
 constexpr int kTopkMaxK = 496;              /* four waves' thresholds need KP = k + 16 <= 4 * 128 */
+constexpr int kTopkHcapMax = 1024;          /* history capacity of a launch (longer histories take the pre-pass) */
 
 /* What each slice workgroup publishes (relaxed agent-scope atomic stores). */
 struct TopkSlot {

@@ -256,28 +256,71 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     if (t < 16) misc[t] = 0;                       /* (16.. are written before they are read) */
 
     /* penalty patches of the ids inside this slice: misc[0] entries of
-     * (pid, pval), their groups' bits in gbits, misc[11] of them allowed by the mask */
-    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
-    auto build_patches_slice = [&]() {
-        if (t < nh) hl[t] = hid;
-        for (int i = t + T; i < nh; i += T) hl[i] = hist[i];
+     * (pid, pval), their groups' bits in gbits, misc[11] of them allowed by the
+     * mask.  The slice's history entries are counted in an LDS hash table of
+     * their ids (open addressing over 2 * hcap >= 2 * nh slots, so every id has
+     * its slot and probes stay short); the entry that inserted an id computes
+     * its patch once every count is in: the patch depends only on the id, its
+     * count, its logit and its mask word, so any one occurrence may compute it.
+     * Keys span hsort and pid, counts pval and pcnt (carved back to back, each
+     * hcap words, a multiple of 16 bytes); pid and pval are reused for the
+     * patch list only after the counts have been read. */
+    int *hkey = (int *)L.hsort;
+    int *hcnt = (int *)L.pval;
+    const int hslots = 2 * p.plan.hcap;            /* a power of two */
+    const int hshift = 32 - (31 - __clz(hslots));
+    constexpr int kPer = kTopkHcapMax / kTopkThreads;   /* history entries per thread (nh <= hcap) */
+    auto stage_history = [&]() {
+        for (int i = t; i < hslots; i += T) { hkey[i] = -1; hcnt[i] = 0; }
         __syncthreads();
-        for (int i = t; i < nh; i += T) {         /* in-slice occurrences, first occurrence only */
-            const int id = hl[i];
+    };
+    auto count_patches = [&]() {
+        int oslot[kPer], oid[kPer];
+        float ov[kPer];
+        uint32_t om[kPer];
+        /* the first T entries from registers (read early), the rest loaded here */
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            const int i = t + k * T;
+            oslot[k] = -1;
+            oid[k] = -1;
+            ov[k] = 0.0f;
+            om[k] = 0xffffffffu;
+            if (i >= nh) continue;
+            const int id = k == 0 ? hid : hist[i];
             if (id < s0 || id >= s1) continue;
-            float v = i == t ? hval : lg[id];      /* entries past the first T: in flight during the count */
-            const uint32_t mword = i == t ? hmw : (mk ? mk[id >> 5] : 0xffffffffu);
-            bool first = true;
-            int cnt = 0;
-            for (int j = 0; j < nh; j++) {
-                const int o = hl[j];
-                if (o == id) { cnt++; if (j < i) first = false; }
+            oid[k] = id;
+            if (k == 0) {
+                ov[k] = hval;
+                om[k] = hmw;
+            } else {
+                ov[k] = lg[id];
+                om[k] = mk ? mk[id >> 5] : 0xffffffffu;
             }
-            if (!first) continue;
-            const bool allowed = (mword >> (id & 31)) & 1u;
+            uint32_t h = ((uint32_t)id * 0x9E3779B1u) >> hshift;
+            bool found = false;
+            for (int probe = 0; probe < hslots && !found; probe++) {
+                const int old = atomicCAS(&hkey[h], -1, id);
+                if (old == -1) oslot[k] = (int)h;
+                if (old == -1 || old == id) found = true;
+                else h = (h + 1) & (uint32_t)(hslots - 1);
+            }
+            if (found) atomicAdd(&hcnt[h], 1);
+        }
+        __syncthreads();
+        int cnt[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; k++) cnt[k] = oslot[k] >= 0 ? hcnt[oslot[k]] : 0;
+        __syncthreads();                           /* counts read: pid and pval are free */
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            if (oslot[k] < 0) continue;
+            const int id = oid[k];
+            float v = ov[k];
+            const bool allowed = (om[k] >> (id & 31)) & 1u;
             if (CAP) v = dlk_softcap_glibc(v, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
             if (!allowed) v = -INFINITY;
-            v = penalised(p, v, cnt);
+            v = penalised(p, v, cnt[k]);
             const int at = atomicAdd(&misc[0], 1);
             if (at < p.plan.hcap) { L.pid[at] = id; L.pval[at] = v; }
             if (allowed) atomicAdd(&misc[11], 1);
@@ -285,7 +328,10 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         }
         __syncthreads();
     };
-    if (GREEDY) build_patches_slice();             /* greedy streams exact values */
+    if (GREEDY) {                                  /* greedy streams exact values */
+        stage_history();
+        count_patches();
+    }
     int np = GREEDY ? min(misc[0], p.plan.hcap) : 0;
 
     /* ---- 2. stream the slice -------------------------------------------- */
@@ -407,7 +453,8 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
             atomicAdd(&misc[3], wn);
             if (spc) misc[8] = 1;
         }
-        build_patches_slice();
+        stage_history();
+        count_patches();
         np = min(misc[0], p.plan.hcap);
         float pmax = -INFINITY;
         int pn = 0, pirr = 0;
