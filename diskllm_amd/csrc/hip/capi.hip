@@ -282,6 +282,8 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     if (G > kFullMaxG) return 1;
     const int S = ept * T;
     if (p.n_out > S) return 1;
+    /* (the no-wait test instance: 16 elements per thread, no soft-cap) */
+    if (no_wait && (ept != 16 || p.cap > 0.0f)) return DLK_ERR_UNSUPPORTED;
     const int nch = S / 64;
     FullParams f;
     memset(&f, 0, sizeof(f));
@@ -289,7 +291,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     f.S = S;
     f.stage_cap = 64;
     f.force_exact = force_exact;
-    f.spin_limit = no_wait ? 0u : kFullSpinLimit;
+    f.no_wait = no_wait;
     /* carve order of full_kernel: sbits, spre, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
      * tab, tbase, rres, rbase, pc, misc, md */
     const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +

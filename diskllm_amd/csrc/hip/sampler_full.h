@@ -52,9 +52,8 @@ struct FullParams {
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
     size_t fb_bytes;
     int force_exact;   /* test hook: send every row through the exact fallback */
-    uint32_t spin_limit;   /* polls after the first before a wait gives up: kFullSpinLimit; 0 (test
-                              hook) makes every wait give up at its first poll that finds a word
-                              not yet written, which sets DLK_STATUS_SYNC_TIMEOUT */
+    int no_wait;       /* test hook: launch the instance whose waits give up at their first poll
+                          that finds a word not yet written (DLK_STATUS_SYNC_TIMEOUT) */
 };
 
 }  // namespace dlk

@@ -70,12 +70,16 @@ DLK_DEV float wave_max(float v) { return wave_max_dpp(v); }
  * between launches. */
 constexpr uint64_t kReady = 1ull << 63;
 
+/* A draw range that starts past the top-p cut (no candidate base is this value:
+ * a base is the bits of a non-negative float less 32, or 0). */
+constexpr uint32_t kPastX = 0xffffffffu;
+
 /* Waits until word idx[k] (k < K) of every workgroup of the row carries kReady
  * and copies it, flag cleared, into pc[h * kPubWords + idx[k]] for the whole
  * workgroup.  Wave 0 polls, a word per lane; the wait is bounded. */
-template <int K>
+template <uint32_t LIMIT, int K>
 __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const int (&idx)[K], uint64_t *pc,
-                                           uint32_t *status, uint32_t spin_limit) {
+                                           uint32_t *status) {
     if (wave_id() == 0) {
         const int lane = lane_id(), n = G * K;
         for (int b = 0; b < n; b += 64) {
@@ -87,7 +91,7 @@ __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const 
             while (true) {
                 if (act && !(w & kReady)) w = at_ld64(&pubrow[off]);
                 if (ballot(act && !(w & kReady)) == 0) break;
-                if (++spins > spin_limit) {
+                if (++spins > LIMIT) {
                     if (lane == 0 && status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
                     break;
                 }
@@ -190,8 +194,11 @@ DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     return base + inc;
 }
 
-template <int EPT, bool CAP>
+/* NOWAIT (a test instance): every wait gives up at its first poll that finds a
+ * word not yet written, which sets DLK_STATUS_SYNC_TIMEOUT. */
+template <int EPT, bool CAP, bool NOWAIT = false>
 __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
+    constexpr uint32_t kLimit = NOWAIT ? 0u : kFullSpinLimit;
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
     const int G = f.G, T = kFullThreads;
@@ -386,7 +393,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     {
         const int idx[1] = {kPubMax};
-        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
     }
     float M = -INFINITY;
     bool row_bad = false;
@@ -430,7 +437,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     /* ---- B: softmax normaliser ------------------------------------------ */
     {
         const int idx[1] = {kPubE};
-        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
     }
     double Sapx = 0.0;
     for (int h = 0; h < G; h++) Sapx += u2d(pc[h * kPubWords + kPubE]);
@@ -494,7 +501,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             }
             {
                 const int idx[3] = {kPubS2, kPubA2, kPubN2};
-                row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
+                row_gather<kLimit>(pubrow, G, idx, pc, p.status);
             }
             double S2 = 0.0, SA = 0.0;
             int64_t nkeep = 0;
@@ -542,7 +549,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
          *      and certifies them and hands them to the others ----------------- */
         {
             const int idx[2] = {kPubP, kPubP0};
-            row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
+            row_gather<kLimit>(pubrow, G, idx, pc, p.status);
         }
         for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
         const double U = 0x1p-53;
@@ -665,7 +672,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 uint32_t spins = 0;
                 const uint64_t *src = &pubrow[hx * kPubWords + kPubX];
                 while (!((wv = at_ld64(src)) & kReady)) {
-                    if (++spins > f.spin_limit) {
+                    if (++spins > kLimit) {
                         if (lane == 0 && p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
                         wv = kReady | 0x7fffffffull;
                         break;
@@ -857,7 +864,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      *      exact start value (exact for slice 0: the sum starts at 0) ------- */
     {
         const int idx[1] = {kPubF};
-        row_gather(pubrow, G, idx, pc, p.status, f.spin_limit);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
     }
     double Phat = 0.0;
     for (int h = 0; h < g; h++) Phat += u2d(pc[h * kPubWords + kPubF]);
@@ -902,7 +909,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      *      element-level chunk is a table lookup.  A lane that leaves what the
      *      prediction covers (another binade, a value outside a table, a crossing
      *      in an unstaged chunk) is marked -2.  Wave 0 then composes the ranges:
-     *      each range's lane for the value the previous range ended with ------- */
+     *      each range's lane for the value the previous range ended with; a
+     *      range that starts past x adds nothing to any start value and is
+     *      passed over (its window would only test the prediction at x) ----- */
     const int nch_loc = x < s0 ? 0 : min(nch, ((x - s0) >> 6) + 1);
     const int nseg = misc[21];
     const int per = (nseg + T / 64 - 1) / (T / 64);
@@ -981,7 +990,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             }
         }
         rres[w * 64 + lane] = make_int2((int)cb, tok);
-        if (lane == 0) rbase[w] = rb;
+        if (lane == 0) rbase[w] = c0 >= nch_loc ? kPastX : rb;
     }
     __syncthreads();
     if (wave_id() == 0) {
@@ -994,7 +1003,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         int tok = -1;
         for (int w = 0; w < nrng; w++) {
             if (ballot(tok == -1) == 0) break;
-            if (tok != -1) continue;
+            if (tok != -1 || rbase[w] == kPastX) continue;
             const uint32_t d = cb - rbase[w];
             if (d >= 64u) {
                 tok = -2;
@@ -1096,10 +1105,19 @@ int ept_index(int ept) { return ept == 16 ? 0 : ept == 24 ? 1 : ept == 32 ? 2 : 
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
     using namespace dlk;
     static int set[2][5] = {{0, 0, 0, 0, 0}, {0, 0, 0, 0, 0}};
+    static int set_nw = 0;
     const int which = ept_index(ept), cap = f->p.cap > 0.0f ? 1 : 0;
     if (which < 0) return -1;
     const void *fn = cap ? full_fn<true>(which) : full_fn<false>(which);
-    if (!set[cap][which]) {
+    if (f->no_wait) {
+        /* the test instance exists for 16 elements per thread, no soft-cap */
+        if (ept != 16 || cap) return -2;
+        fn = (const void *)full_kernel<16, false, true>;
+        if (!set_nw) {
+            if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
+            set_nw = 1;
+        }
+    } else if (!set[cap][which]) {
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
         set[cap][which] = 1;
     }

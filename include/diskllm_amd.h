@@ -70,7 +70,9 @@ typedef struct {
 #define DLK_PATH_FULL_EXACT 2  /* fused full-vocabulary kernel with every row finished by its exact fallback */
 #define DLK_PATH_FULL_NO_WAIT 3  /* fused full-vocabulary kernel whose cross-workgroup waits give up at the
                                    first poll that finds a word not yet written: forces the
-                                   DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid) */
+                                   DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid).
+                                   Shapes whose slices hold 16 entries per thread, no soft-cap;
+                                   others return DLK_ERR_UNSUPPORTED */
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */
