@@ -128,6 +128,26 @@ def sample(db: DeviceBatch, params: Optional[_lib.SampleParams] = None, stream: 
     _lib.check(rc, "dlk_sample")
 
 
+def sampler(db: DeviceBatch, params: Optional[_lib.SampleParams] = None, stream: Optional[int] = None):
+    """A callable that makes the dlk_sample call of sample() with its argument
+    structures built once: a loop of calls then costs the C call alone (timing
+    loops; the batch's buffers must stay where they are)."""
+    w = db.w
+    p = params if params is not None else params_of(w)
+    b = batch_struct(db)
+    f = _lib.lib().dlk_sample
+    rows, vocab = db.logits.shape[0], w.vocab
+    sh = stream if stream is not None else stream_handle()
+    bp, pp = C.byref(b), C.byref(p)
+
+    def run() -> None:
+        rc = f(bp, rows, vocab, pp, sh)
+        if rc != 0:
+            _lib.check(rc, "dlk_sample")
+    run.keep = (b, p)
+    return run
+
+
 def results(db: DeviceBatch) -> dict:
     torch.cuda.synchronize()
     out = dict(ids=db.out_ids.cpu().numpy(), states=db.rng.cpu().numpy().view(np.uint64),
