@@ -15,10 +15,13 @@ namespace dlk {
 
 constexpr int kDfaRegBytes = 16;          /* token bytes held in registers; longer tokens read the rest */
 
-/* One thread per token and a group of R rows per block (grid.y: the row
- * groups, so that enough waves hide the lookups' latency; R = 8 for up to 16
- * rows, 16 above: 13.2 against 15.3 us for 16 rows over 151,936 tokens, 39.7
- * against 44.6 us for 64 rows over 262,144).  The rows are
+/* One thread per token; the rows in groups of R (R = 8 for up to 16 rows, 16
+ * above: 13.2 against 15.3 us for 16 rows over 151,936 tokens, 39.7 against
+ * 44.6 us for 64 rows over 262,144), gpb groups per block one after another
+ * (grid.y: the blocks of groups).  A block stages the table and reads its
+ * tokens' bytes once for all its groups, so the host gives a block as many
+ * groups as keep the grid at about 1,024 blocks or more (64 rows over 262,144
+ * tokens: all four groups in one block, 34.6 against 40.4 us).  The rows are
  * stepped together: at each byte position every row takes one table lookup
  * (independent of the other rows'), so a step is 16 LDS reads in flight rather
  * than one dependent chain per row.  The table is staged with state 0's row all
@@ -28,8 +31,9 @@ template <int R>
 __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restrict__ off,
                                                        const uint8_t *__restrict__ bytes, int V,
                                                        const uint8_t *__restrict__ trans, int n_states,
-                                                       const int32_t *__restrict__ states, int n_rows, int eos_id,
-                                                       uint64_t accept, uint32_t *__restrict__ out, int64_t ld) {
+                                                       const int32_t *__restrict__ states, int n_rows, int gpb,
+                                                       int eos_id, uint64_t accept, uint32_t *__restrict__ out,
+                                                       int64_t ld) {
     extern __shared__ uint8_t tt[];
     const int n_tt = n_states * 256;
     for (int i = threadIdx.x * 4; i < n_tt; i += blockDim.x * 4) {
@@ -57,8 +61,8 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
     for (int m = 32; m >= 1; m >>= 1) wl = max(wl, (uint32_t)shfl_xor((int)wl, m));
     const int wbase = (tok - lane) >> 5;          /* first word of this wave's 64 tokens */
     __syncthreads();
-    {
-        const int r0 = blockIdx.y * R;
+    const int r_end = min(n_rows, (int)(blockIdx.y + 1) * gpb * R);
+    for (int r0 = blockIdx.y * gpb * R; r0 < r_end; r0 += R) {
         const int nr = min(n_rows - r0, R);
         uint32_t st[R];
 #pragma unroll
@@ -110,12 +114,14 @@ extern "C" int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab
     if (mask_ld < (vocab + 31) / 32) return DLK_ERR_INVALID;
     if (((uintptr_t)trans & 3) != 0) return DLK_ERR_INVALID;
     const int R = n_rows <= 16 ? 8 : 16;
-    dim3 grid((vocab + 255) / 256, (n_rows + R - 1) / R);
+    const int n_groups = (n_rows + R - 1) / R, tok_blocks = (vocab + 255) / 256;
+    int gpb = (int)std::min<int64_t>(n_groups, std::max<int64_t>(1, (int64_t)tok_blocks * n_groups / 1024));
+    dim3 grid(tok_blocks, (n_groups + gpb - 1) / gpb);
     if (R == 8)
         hipLaunchKernelGGL(dlk::dfa_mask_kernel<8>, grid, dim3(256), (size_t)n_states * 256, stream, off, bytes, vocab,
-                           trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+                           trans, n_states, states, n_rows, gpb, eos_id, accept_mask, out_mask, mask_ld);
     else
         hipLaunchKernelGGL(dlk::dfa_mask_kernel<16>, grid, dim3(256), (size_t)n_states * 256, stream, off, bytes,
-                           vocab, trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+                           vocab, trans, n_states, states, n_rows, gpb, eos_id, accept_mask, out_mask, mask_ld);
     return hipGetLastError() == hipSuccess ? DLK_OK : DLK_ERR_HIP;
 }
