@@ -21,7 +21,7 @@ constexpr int kDfaRegBytes = 16;          /* token bytes held in registers; long
  * (grid.y: the blocks of groups).  A block stages the table and reads its
  * tokens' bytes once for all its groups, so the host gives a block as many
  * groups as keep the grid at about 1,024 blocks or more (64 rows over 262,144
- * tokens: all four groups in one block, 34.6 against 40.4 us).  The rows are
+ * tokens: all four groups in one block, 35.6 against 40.2 us).  The rows are
  * stepped together: at each byte position every row takes one table lookup
  * (independent of the other rows'), so a step is 16 LDS reads in flight rather
  * than one dependent chain per row.  The table is staged with state 0's row all
