@@ -816,10 +816,29 @@ __device__ __forceinline__ int pipeline(const RowParams &p, const B &base, int n
     return d.pos >= 0 ? d.pos : last_kept;
 }
 
+/* The reference's running double sum of the lanes' values in lane order
+ * (finite, non-negative; a 0 adds nothing), as an inclusive prefix in every
+ * lane -- by a wave scan, when that is provably the same: if every value is a
+ * whole multiple of U = 2^(k-52), where 2^k > 64 * max >= every prefix, each
+ * prefix is a multiple of U below 2^(k+1), so a double, every addition of the
+ * sequential loop is exact, and a scan in any order gives the same numbers.
+ * Returns false when the condition fails (the caller runs the loop). */
+DLK_DEV bool exact_prefix_d(float v, double &pre) {
+    const float mx = wave_max_dpp(v);
+    if (!(mx < INFINITY)) return false;
+    int k = 0;
+    (void)frexp(64.0 * (double)mx, &k);       /* 64 * max < 2^k */
+    const double sc = ldexp((double)v, 52 - k);
+    if (ballot(!(sc == trunc(sc))) != 0) return false;
+    pre = wave_incl_scan_d((double)v);
+    return true;
+}
+
 /* pipeline for n <= 64 candidates, by one wave (lane j holds candidate j): the
- * reference's sequential sums (src/sampler.c:177-233) run literally, in the
- * same order, with every lane repeating them on values read lane by lane.  No
- * block barrier; the caller broadcasts pos and S. */
+ * reference's sequential sums (src/sampler.c:177-233) in the same order -- a
+ * double sum by exact_prefix_d's scan where that gives the same number, else
+ * literally, every lane repeating it on values read lane by lane; the draw's
+ * float sum literally.  No block barrier; the caller broadcasts pos and S. */
 template <class B>
 __device__ __forceinline__ int pipeline_small(const RowParams &p, const B &base, int n, float r, Scal &S) {
     const int lane = lane_id();
@@ -827,8 +846,12 @@ __device__ __forceinline__ int pipeline_small(const RowParams &p, const B &base,
     S.minp_on = p.minp_on; S.minp_all = 0; S.topp_on = p.topp_on; S.cut = n - 1;
     const float e = lane < n ? base.e(lane) : 0.0f;
     /* softmax, :177-185 */
-    double sum = 0.0;
-    for (int j = 0; j < n; j++) sum += (double)readlanef(e, j);
+    double sum = 0.0, pre = 0.0;
+    if (exact_prefix_d(e, pre)) {
+        sum = u2d(readlane64(d2u(pre), 63));
+    } else {
+        for (int j = 0; j < n; j++) sum += (double)readlanef(e, j);
+    }
     S.inv = (float)(1.0 / sum);
     const float pj = e * S.inv;
     /* min-p, :188-202: survivors in order, all kept if none survives */
@@ -839,8 +862,12 @@ __device__ __forceinline__ int pipeline_small(const RowParams &p, const B &base,
         S.cut = S.minp_all ? n - 1 : 63 - __builtin_clzll(surv);
         const bool kept = lane < n && (S.minp_all || ((surv >> lane) & 1ull));
         double s2 = 0.0;
-        for (int j = 0; j < n; j++)
-            if (S.minp_all || ((surv >> j) & 1ull)) s2 += (double)readlanef(pj, j);
+        if (exact_prefix_d(kept ? pj : 0.0f, pre)) {
+            s2 = u2d(readlane64(d2u(pre), 63));
+        } else {
+            for (int j = 0; j < n; j++)
+                if (S.minp_all || ((surv >> j) & 1ull)) s2 += (double)readlanef(pj, j);
+        }
         S.inv2 = (float)(1.0 / s2);
         t = kept ? pj * S.inv2 : 0.0f;
     }
@@ -852,6 +879,11 @@ __device__ __forceinline__ int pipeline_small(const RowParams &p, const B &base,
         if (p.top_p <= 0.0f) {
             x = S.minp_on && !S.minp_all ? __builtin_ctzll(ballot(lane < n && pj >= S.min_p)) : 0;
             s3 = (double)readlanef(t, x);
+        } else if (exact_prefix_d(lane <= last_kept ? t : 0.0f, pre)) {
+            /* the first position whose prefix reaches top_p, else all kept */
+            const uint64_t hit = ballot(lane <= last_kept && (float)pre >= p.top_p);
+            x = hit ? __builtin_ctzll(hit) : last_kept;
+            s3 = u2d(readlane64(d2u(pre), x));
         } else {
             double cumul = 0.0;
             for (int j = 0; j <= last_kept; j++) {

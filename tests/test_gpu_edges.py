@@ -269,3 +269,23 @@ def test_sync_timeout_path(cuda):
         for r in range(w.rows):
             assert int(res["ids"][r]) == ref[r]["token"], (cycle, r)
             assert int(res["states"][r]) == ref[r]["state"], (cycle, r)
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_topk_sums_both_ways(cuda, path):
+    """Top-k rows whose k candidates' softmax terms either are all whole
+    multiples of the running sum's ulp (the one-wave pipeline sums them by a
+    wave scan) or are not (terms down to 2^-40 of the maximum: it runs the
+    reference's loops); min-p and top-p on both, against the oracle."""
+    V, k = 40000, 48
+    rng = np.random.default_rng(11)
+    lg = rng.normal(0, 1, size=(6, V)).astype(np.float32)
+    top = rng.choice(V, size=(6, k), replace=False)
+    for r in range(6):
+        if r % 2 == 0:
+            lg[r, top[r]] = 20.0 + rng.normal(0, 0.5, size=k).astype(np.float32)       # close together
+        else:
+            lg[r, top[r]] = 20.0 + np.linspace(0.0, -28.0, k).astype(np.float32)      # spread far apart
+    for top_p, min_p in ((0.9, 0.0), (1.0, 1e-6), (0.95, 1e-7)):
+        w = make("topk_sums", 6, V, seed=12, temperature=1.0, top_k=k, top_p=top_p, min_p=min_p, logits=lg, n_out=8)
+        run_and_check(w, path)
