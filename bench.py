@@ -36,7 +36,7 @@ def fused_kernel_name(rows: int, vocab: int) -> str:
     G = min(16, max(1, (256 + rows - 1) // rows))
     ept = (vocab + G * 1024 - 1) // (G * 1024)
     ept = next(e for e in (16, 24, 32, 40, 48) if ept <= e or e == 48)
-    return f"dlk::full_kernel<{ept}, false>"
+    return f"dlk::full_kernel<{ept}, false, false>"
 
 
 # The dominant kernel of each workload and its committed traffic summary.
