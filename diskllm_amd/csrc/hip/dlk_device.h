@@ -155,12 +155,6 @@ DLK_DEV uint32_t wave_scan_sat_u32(uint32_t x, uint32_t cap) {
     return x;
 }
 
-/* Wave-wide sum (any order) of a double. */
-DLK_DEV double wave_sum(double v) {
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-    return v;
-}
-
 }  // namespace dlk
 
 #endif

@@ -158,12 +158,22 @@ DLK_DEV uint64_t ceil_div_pow2(double v, int ue) {
     return (mv >> s) + ((mv & ((1ull << s) - 1)) != 0);
 }
 
+/* The lanes' pairs composed in lane order, inclusive: DPP row shifts, then row
+ * broadcasts (a lane with no source receives {0, 0}, the identity of
+ * compose; the left operand is always the lower lanes' part, so the order of
+ * the composition is kept). */
+template <int CTRL, int ROWS = 0xf, bool BC = true>
+DLK_DEV Pair dpp_pair(Pair x) {
+    return Pair{dpp_u64<CTRL, ROWS, BC>(x.a0), dpp_u64<CTRL, ROWS, BC>(x.a1)};
+}
 DLK_DEV Pair wave_incl_scan(Pair x, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        uint64_t l0 = shfl_up(x.a0, d), l1 = shfl_up(x.a1, d);
-        if (lane >= d) x = compose(Pair{l0, l1}, x);
-    }
+    (void)lane;
+    x = compose(dpp_pair<kDppRowShr1>(x), x);
+    x = compose(dpp_pair<kDppRowShr2>(x), x);
+    x = compose(dpp_pair<kDppRowShr4>(x), x);
+    x = compose(dpp_pair<kDppRowShr8>(x), x);
+    x = compose(dpp_pair<kDppRowBcast15, 0xa, false>(x), x);
+    x = compose(dpp_pair<kDppRowBcast31, 0xc, false>(x), x);
     return x;
 }
 
@@ -186,8 +196,8 @@ __device__ __forceinline__ void chunk_prefix(int n, const QF &q, double *P, doub
     for (int c = w; c < nch; c += nw) {
         int i = c * 64 + lane;
         double v = i < n ? (double)q(i) : 0.0;
-        v = wave_sum(v);
-        if (lane == 0) P[c] = v;
+        v = wave_incl_scan_d(v);                /* (any order: P only predicts binades) */
+        if (lane == 63) P[c] = v;
     }
     __syncthreads();
     /* exclusive scan over nch values: each thread a contiguous run. */
@@ -196,12 +206,7 @@ __device__ __forceinline__ void chunk_prefix(int n, const QF &q, double *P, doub
     const int b0 = t * per, b1 = min(nch, b0 + per);
     double loc = 0.0;
     for (int c = b0; c < b1; c++) loc += P[c];
-    double inc = loc;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        double o = shfl_up(inc, d);
-        if (lane >= d) inc += o;
-    }
+    const double inc = wave_incl_scan_d(loc);
     if (lane == 63) red[w] = inc;
     __syncthreads();
     double wbase = 0.0;

@@ -356,11 +356,7 @@ __device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist,
             const int per = nb / 64;
             uint32_t loc = 0;
             for (int b = 0; b < per; b++) loc += hist[lane * per + b];
-            uint32_t inc = loc;
-            for (int d = 1; d < 64; d <<= 1) {
-                uint32_t o = shfl_up(inc, d);
-                if (lane >= d) inc += o;
-            }
+            const uint32_t inc = wave_scan_sat_u32(loc, 0xffffffffu);
             uint32_t exc = inc - loc;
             bool hit = exc < (uint32_t)krem && inc >= (uint32_t)krem;
             uint64_t bal = ballot(hit);
