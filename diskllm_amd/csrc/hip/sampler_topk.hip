@@ -218,12 +218,23 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     auto gpos = [&](int b, int j) { return s0 + 4 * (t + (4 * b + j) * T); };
     float4 xa[4];
     uint32_t ma[4];
+    /* A batch's loads: the mask words unshifted (the shift waits for the
+     * load, and a wait here would keep one group in flight instead of the
+     * batch); a batch wholly inside the slice without per-lane guards. */
+    const int msh = (s0 + 4 * t) & 31;             /* bit of a group's first entry in its mask word */
     auto load_batch = [&](float4 (&x)[4], uint32_t (&m)[4], int b) {
+        if (gpos(b, 0) - 4 * t + 16 * T <= s1) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i0 = gpos(b, j);
-            x[j] = load_group(lg, i0, s1);
-            m[j] = (mk && i0 < s1) ? mk[i0 >> 5] >> (i0 & 31) : 0xFu;
+            for (int j = 0; j < 4; j++) x[j] = *(const float4 *)(lg + gpos(b, j));
+#pragma unroll
+            for (int j = 0; j < 4; j++) m[j] = mk ? mk[gpos(b, j) >> 5] : 0xffffffffu;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i0 = gpos(b, j);
+                x[j] = load_group(lg, i0, s1);
+                m[j] = (mk && i0 < s1) ? mk[i0 >> 5] : 0xffffffffu;
+            }
         }
     };
     /* batch 0 first: in flight while the history is read (one register set:
@@ -348,7 +359,8 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
             const int i0 = gpos(b, j);
             /* (non-greedy: the penalised ids stream their raw logits; the
              * patches come after the stream) */
-            const uint32_t live = GREEDY ? group_live(m[j], gbits, L.pid, np, i0, s0, s1) : range_live(m[j], i0, s1);
+            const uint32_t mw = m[j] >> msh;
+            const uint32_t live = GREEDY ? group_live(mw, gbits, L.pid, np, i0, s0, s1) : range_live(mw, i0, s1);
             const float4 v = x[j];
             float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
