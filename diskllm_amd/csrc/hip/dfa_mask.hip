@@ -14,6 +14,7 @@
 namespace dlk {
 
 constexpr int kDfaRegBytes = 16;          /* token bytes held in registers; longer tokens read the rest */
+constexpr int kDfaStageWords = 16;        /* table words a thread loads at once while staging */
 
 /* One thread per token; the rows in groups of R (R = 8 for up to 16 rows, 16
  * above: 13.2 against 15.3 us for 16 rows over 151,936 tokens, 39.7 against
@@ -36,13 +37,6 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
                                                        int64_t ld) {
     extern __shared__ uint8_t tt[];
     const int n_tt = n_states * 256;
-    for (int i = threadIdx.x * 4; i < n_tt; i += blockDim.x * 4) {
-        uint32_t w = i < 256 ? 0u : *(const uint32_t *)(trans + i);
-        if (n_states < 256)
-            for (int k = 0; k < 4; k++)
-                if (((w >> (8 * k)) & 255u) >= (uint32_t)n_states) w &= ~(255u << (8 * k));
-        *(uint32_t *)(tt + i) = w;
-    }
     const int tok = blockIdx.x * blockDim.x + threadIdx.x;
     const int lane = lane_id();
     const int W = (V + 31) >> 5;
@@ -51,10 +45,31 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
         b0 = off[tok];
         len = off[tok + 1] - b0;
     }
-    /* the token's first bytes, every load issued at once */
+    /* the token's first bytes, every load issued at once (they land while the
+     * table is staged) */
     uint32_t by[kDfaRegBytes];
 #pragma unroll
     for (int j = 0; j < kDfaRegBytes; j++) by[j] = (uint32_t)j < len ? bytes[b0 + j] : 0u;
+    /* the table: kDfaStageWords words per thread loaded before any is stored,
+     * so one round trip stages up to 64 states */
+    for (int i0 = threadIdx.x * 4; i0 < n_tt; i0 += blockDim.x * 4 * kDfaStageWords) {
+        uint32_t w[kDfaStageWords];
+#pragma unroll
+        for (int u = 0; u < kDfaStageWords; u++) {
+            const int i = i0 + u * (int)blockDim.x * 4;
+            w[u] = i >= 256 && i < n_tt ? *(const uint32_t *)(trans + i) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kDfaStageWords; u++) {
+            const int i = i0 + u * (int)blockDim.x * 4;
+            if (i >= n_tt) break;
+            uint32_t x = w[u];
+            if (n_states < 256)
+                for (int k = 0; k < 4; k++)
+                    if (((x >> (8 * k)) & 255u) >= (uint32_t)n_states) x &= ~(255u << (8 * k));
+            *(uint32_t *)(tt + i) = x;
+        }
+    }
     const bool walk = tok < V && tok != eos_id && len > 0;
     /* steps every lane of the wave may need: the wave's longest token, up to kDfaRegBytes */
     uint32_t wl = len < (uint32_t)kDfaRegBytes ? len : (uint32_t)kDfaRegBytes;
