@@ -143,6 +143,20 @@ DLK_DEV float wave_max_dpp(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowBcast31, 0xc, 0xf, false)));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+/* Wave-wide minimum and maximum of a u32 (DPP row shifts, then row
+ * broadcasts; lanes with no source take the identity). */
+template <bool MIN>
+DLK_DEV uint32_t wave_minmax_u32(uint32_t v) {
+    const int id = MIN ? -1 : 0;
+    uint32_t o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowShr1, 0xf, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowShr2, 0xf, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowShr4, 0xf, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowShr8, 0xf, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowBcast15, 0xa, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    o = (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, kDppRowBcast31, 0xc, 0xf, false); v = MIN ? min(v, o) : max(v, o);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 /* Inclusive wave prefix with saturation at `cap` (values <= cap). */
 DLK_DEV uint32_t wave_scan_sat_u32(uint32_t x, uint32_t cap) {
     uint32_t t;

@@ -661,14 +661,18 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     }
     uint32_t *sw = (uint32_t *)selh;               /* max, argmax, nfin, first_nan per slice (G <= 64) */
     if (t < G) {
+        /* every word loaded before any is stored (one round trip, not seven) */
         const TopkSlot *s = f.slots + ((int64_t)row * G + t);
-        sk[3 * t + 0] = get32(&s->kept);
-        sk[3 * t + 1] = get32(&s->complete);
-        sk[3 * t + 2] = get32(&s->last_key);
-        sw[t] = get32(&s->max_bits);
-        sw[64 + t] = get32(&s->argmax);
-        sw[128 + t] = get32(&s->nfin);
-        sw[192 + t] = get32(&s->first_nan);
+        const uint32_t kept_h = get32(&s->kept), complete_h = get32(&s->complete), last_h = get32(&s->last_key);
+        const uint32_t max_h = get32(&s->max_bits), arg_h = get32(&s->argmax), nfin_h = get32(&s->nfin);
+        const uint32_t nan_h = get32(&s->first_nan);
+        sk[3 * t + 0] = kept_h;
+        sk[3 * t + 1] = complete_h;
+        sk[3 * t + 2] = last_h;
+        sw[t] = max_h;
+        sw[64 + t] = arg_h;
+        sw[128 + t] = nfin_h;
+        sw[192 + t] = nan_h;
     }
     uint32_t *tau = sk + 3 * G, *tau2 = sk + 3 * G + 1;
     if (t == 0) { pub32(&f.counters[row], 0u); *tau = 0xffffffffu; *tau2 = 0u; misc[46] = 0; }
@@ -745,18 +749,31 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
          * the top k */
         const int cq = (k + G - 1) / G;
         const bool all_cq = __popcll(ballot(lane < G && (int)sk[3 * lane] >= cq)) == (unsigned)G;
+        /* (list h, slot j) of entry i = t + u * T, stepped without a division;
+         * tau and tau2 reduced in the wave first (one LDS atomic per wave) */
+        const int qT = T / KP, rT = T - qT * KP;
+        int h = t / KP, j = t - h * KP;
+        uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
         for (int u = 0; u < kMergePerThread; u++) {
             const int i = t + u * T;
-            const int h = i / KP, j = i - h * KP;
             if (i < GK && j < (int)sk[3 * h]) {
                 cv[u] = ((uint64_t)desc_key((key_value((uint32_t)(cv[u] >> 32)) - M) * R.inv_t) << 32) |
                         (cv[u] & 0xffffffffull);
-                if (j == k - 1) atomicMin(tau, (uint32_t)(cv[u] >> 32));
-                if (j == cq - 1) atomicMax(tau2, (uint32_t)(cv[u] >> 32));
+                if (j == k - 1) kmin = min(kmin, (uint32_t)(cv[u] >> 32));
+                if (j == cq - 1) kmax = max(kmax, (uint32_t)(cv[u] >> 32));
             } else {
                 cv[u] = ~0ull;
             }
+            h += qT;
+            j += rT;
+            if (j >= KP) { j -= KP; h++; }
+        }
+        kmin = wave_minmax_u32<true>(kmin);
+        kmax = wave_minmax_u32<false>(kmax);
+        if (lane == 0) {
+            if (kmin != 0xffffffffu) atomicMin(tau, kmin);
+            if (kmax != 0u) atomicMax(tau2, kmax);
         }
         __syncthreads();
         const uint32_t tk = all_cq ? min(*tau, *tau2) : *tau;
