@@ -271,6 +271,7 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     /* min-p with the cut after the first kept entry (it may lie in any slice): the row kernel */
     if (p.minp_on && p.topp_on && p.top_p <= 0.0f) return 1;
     if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
+    if (p.plan.hcap > T) return 1;                     /* one history id per thread, loaded first */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     if (vocab < 8192 || (vocab & 3) != 0) return 1;   /* whole 16-byte groups per row */
     int G = (256 + rows - 1) / rows;
@@ -292,9 +293,9 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     f.stage_cap = 64;
     f.force_exact = force_exact;
     f.no_wait = no_wait;
-    /* carve order of full_kernel: sbits, spre, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
+    /* carve order of full_kernel: sbits, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
      * tab, tbase, rres, rbase, pc, misc, md */
-    const size_t lds = fixed_lds(p.plan) + 2 * r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
+    const size_t lds = fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
                        2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
                        r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)f.stage_cap * 64 * 4) +
                        r16((size_t)nch * 8) + r16((size_t)nch * 16) + r16((size_t)kMaxTabs * 64 * 8) +

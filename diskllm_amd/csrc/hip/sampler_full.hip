@@ -79,7 +79,7 @@ constexpr uint32_t kPastX = 0xffffffffu;
  * workgroup.  Wave 0 polls, a word per lane; the wait is bounded. */
 template <uint32_t LIMIT, int K>
 __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const int (&idx)[K], uint64_t *pc,
-                                           uint32_t *status) {
+                                           uint32_t *status, int *tflag) {
     if (wave_id() == 0) {
         const int lane = lane_id(), n = G * K;
         for (int b = 0; b < n; b += 64) {
@@ -92,7 +92,10 @@ __device__ __forceinline__ void row_gather(const uint64_t *pubrow, int G, const 
                 if (act && !(w & kReady)) w = at_ld64(&pubrow[off]);
                 if (ballot(act && !(w & kReady)) == 0) break;
                 if (++spins > LIMIT) {
-                    if (lane == 0 && status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
+                    if (lane == 0) {
+                        if (status) atomicOr(status, DLK_STATUS_SYNC_TIMEOUT);
+                        *tflag = 1;
+                    }
                     break;
                 }
             }
@@ -165,23 +168,6 @@ __device__ __forceinline__ double exp_slice(float (&v)[EPT], float M, float inv_
     return tsum;
 }
 
-/* Rank of marked bit li among the marked bits before it. */
-DLK_DEV int slice_rank(const uint32_t *bits, const uint32_t *pre, int li) {
-    return (int)pre[li >> 5] + __popc(bits[li >> 5] & ((1u << (li & 31)) - 1u));
-}
-
-/* Exclusive prefix of per-thread counts in thread order (red: 16 words). */
-DLK_DEV uint32_t block_excl_prefix_u32(uint32_t v, uint32_t *red) {
-    const int lane = lane_id(), w = wave_id();
-    const uint32_t inc = wave_scan_sat_u32(v, 0xffffffffu);
-    if (lane == 63) red[w] = inc;
-    __syncthreads();
-    const uint32_t wt = wave_scan_sat_u32(lane < (int)(blockDim.x / 64) ? red[lane] : 0u, 0xffffffffu);
-    const uint32_t base = w > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)wt, w - 1) : 0u;
-    __syncthreads();
-    return base + inc - v;
-}
-
 /* Inclusive prefix of per-thread 64-bit values in thread order (red: 16 words). */
 DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     const int lane = lane_id(), w = wave_id();
@@ -216,7 +202,6 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     Lds L = make_lds(smem, p.plan);
     unsigned char *q = L.region;
     uint32_t *sbits = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
-    uint32_t *spre = (uint32_t *)carve(q, (size_t)(S / 32) * 4);
     double *ce = (double *)carve(q, (size_t)(nch + 1) * 8);      /* e prefix; later the contributions' prefix */
     int *cbh = (int *)carve(q, (size_t)nch * 4);                 /* chunk binade, kInvalidBinade or kZeroBinade */
     uint32_t *ca = (uint32_t *)carve(q, (size_t)nch * 4);        /* chunk increments on that grid */
@@ -238,29 +223,21 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double *md = (double *)carve(q, 16 * 8);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
-    /* ---- history first: the ids, and for an id inside this slice its logit
-     *      and mask word, gathered before the bulk loads so that the penalties
-     *      are computed while the slice is still in flight ---------------------- */
+    /* ---- history first: the row's ids (one per thread; the host keeps the
+     *      direct history within the workgroup) and, for an id inside this
+     *      slice, its logit and mask word, gathered before the bulk loads ----- */
     const int32_t *hist = nullptr;
     int nh = 0;
     if (p.hist_off) {
         hist = p.hist_ids + p.hist_off[row];
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
-    constexpr int kHistPer = 2;                    /* history ids per thread gathered early */
-    int hid[kHistPer];
-    float gx[kHistPer];
-    uint32_t gm[kHistPer];
-#pragma unroll
-    for (int k = 0; k < kHistPer; k++) hid[k] = t + k * T < nh ? hist[t + k * T] : -1;
-#pragma unroll
-    for (int k = 0; k < kHistPer; k++) {
-        gx[k] = 0.0f;
-        gm[k] = 0xffffffffu;
-        if (hid[k] >= s0 && hid[k] < s1) {
-            gx[k] = lg[hid[k]];
-            if (mk) gm[k] = mk[hid[k] >> 5];
-        }
+    const int hid = t < nh ? hist[t] : -1;
+    float gx = 0.0f;
+    uint32_t gm = 0xffffffffu;
+    if (hid >= s0 && hid < s1) {
+        gx = lg[hid];
+        if (mk) gm = mk[hid >> 5];
     }
 
     /* ---- stream the slice into registers: every load issued before any use */
@@ -268,7 +245,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     uint32_t mwd[EPT / 4];
     load_slice<EPT, 0, EPT / 4>(lg, mk, s0, s1, t, T, raw, mwd);
 
-    if (nh > p.plan.hcap) {
+    if (nh > p.plan.hcap || nh > T) {              /* (the host keeps both) */
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
             if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
@@ -277,70 +254,50 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         return;
     }
     /* ---- penalty patches of the ids inside this slice ------------------- */
+    /* The slice's history entries are counted in an LDS hash table of their
+     * ids (open addressing over 2 * hcap >= 2 * nh slots: every id has its
+     * slot and probes stay short; keys span hsort and pid, counts pval and
+     * pcnt, carved back to back), and a bit per slice element marks the ids.
+     * A patch depends only on the id's count, its logit and its mask word, so
+     * the entry that inserted the id computes it once every count is in, from
+     * the logit and mask word it gathered before the bulk loads, and leaves it
+     * in the slot in place of the count (in straight-line code: the use of the
+     * gathered values then waits only for those loads, and the merge below
+     * takes the slice as it lands).  Two block barriers, where ranking the
+     * marked ids by a scan of the bitmap took six. */
     const int nw = S / 32;
-    int *pfirst = L.pid;                           /* first history position of each patched id */
-    int *hl = (int *)L.hsort;                      /* the row's history, staged in LDS */
+    int *hkey = (int *)L.hsort;
+    uint32_t *hcnt = (uint32_t *)L.pval;
+    const int hslots = 2 * p.plan.hcap;            /* a power of two */
+    const int hshift = 32 - (31 - __clz(hslots));
     for (int i = t; i < nw; i += T) sbits[i] = 0;
-    for (int i = t; i < p.plan.hcap; i += T) { L.pcnt[i] = 0; pfirst[i] = 0x7fffffff; }
-    if (t == 0) misc[5] = 0;
+    for (int i = t; i < hslots; i += T) { hkey[i] = -1; hcnt[i] = 0u; }
+    if (t == 0) { misc[5] = 0; misc[6] = 0; }     /* a NaN / +inf entry; a wait that gave up */
     __syncthreads();
-    for (int i = t; i < nh; i += T) {
-        const int k = (i - t) / T;
-        int id = 0;
-        if (k < kHistPer) {
-#pragma unroll
-            for (int kk = 0; kk < kHistPer; kk++)
-                if (kk == k) id = hid[kk];
-        } else {
-            id = hist[i];
+    int oslot = -1;
+    if (hid >= s0 && hid < s1) {
+        uint32_t h = ((uint32_t)hid * 0x9E3779B1u) >> hshift;
+        for (int probe = 0; probe < hslots; probe++) {
+            const int old = atomicCAS(&hkey[h], -1, hid);
+            if (old == -1) { oslot = (int)h; atomicOr(&sbits[(hid - s0) >> 5], 1u << ((hid - s0) & 31)); }
+            if (old == -1 || old == hid) break;
+            h = (h + 1) & (uint32_t)(hslots - 1);
         }
-        hl[i] = id;
-        if (id >= s0 && id < s1) atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31));
+        atomicAdd(&hcnt[h], 1u);
     }
     __syncthreads();
-    /* patch slot of a marked id = its rank among the marked ids of the slice */
-    {
-        const int per = (nw + T - 1) / T, w0 = t * per;
-        uint32_t cnt = 0;
-        for (int k = 0; k < per; k++)
-            if (w0 + k < nw) cnt += __popc(sbits[w0 + k]);
-        uint32_t base = block_excl_prefix_u32(cnt, (uint32_t *)L.bi);
-        for (int k = 0; k < per; k++)
-            if (w0 + k < nw) { spre[w0 + k] = base; base += __popc(sbits[w0 + k]); }
+    if (oslot >= 0) {
+        float x = gx;
+        if (CAP) x = dlk_softcap_glibc(x, p.cap);
+        if (!((gm >> (hid & 31)) & 1u)) x = -INFINITY;
+        hcnt[oslot] = __float_as_uint(penalize(x, (int)hcnt[oslot], p));
     }
-    __syncthreads();
-    for (int i = t; i < nh; i += T) {
-        const int id = hl[i];
-        if (id >= s0 && id < s1) {
-            const int slot = slice_rank(sbits, spre, id - s0);
-            atomicAdd(&L.pcnt[slot], 1);
-            atomicMin(&pfirst[slot], i);
-        }
-    }
-    __syncthreads();
-    /* the thread of an id's first occurrence applies its penalties (src/sampler.c:21-52) */
-    for (int i = t; i < nh; i += T) {
-        const int id = hl[i];
-        if (id < s0 || id >= s1) continue;
-        const int slot = slice_rank(sbits, spre, id - s0);
-        if (pfirst[slot] != i) continue;
-        const int k = (i - t) / T;
-        float x;
-        uint32_t m;
-        if (k < kHistPer) {
-            x = 0.0f;
-            m = 0u;
-#pragma unroll
-            for (int kk = 0; kk < kHistPer; kk++)
-                if (kk == k) { x = gx[kk]; m = gm[kk]; }
-        } else {
-            x = lg[id];
-            m = mk ? mk[id >> 5] : 0xffffffffu;
-        }
-        if (CAP) x = dlk_softcap_glibc(x, p.cap);  /* the soft-cap first (src/core/context.c:873-876) */
-        if (!((m >> (id & 31)) & 1u)) x = -INFINITY;
-        L.pval[slot] = penalize(x, L.pcnt[slot], p);
-    }
+    /* the patch of a marked id */
+    auto hpatch = [&](int id) {
+        uint32_t h = ((uint32_t)id * 0x9E3779B1u) >> hshift;
+        while (hkey[h] != id) h = (h + 1) & (uint32_t)(hslots - 1);
+        return __uint_as_float(hcnt[h]);
+    };
     const uint64_t st = xorshift64(p.rng[row]);     /* one uniform per sampled row (src/sampler.c:225) */
     const float r = rand_f32_from(st);
     __syncthreads();
@@ -368,11 +325,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int li0 = i0 - s0;
         const uint32_t pb = i0 < s1 ? (sbits[li0 >> 5] >> (li0 & 31)) & 0xFu : 0u;
         if (pb) {
-            /* patch slots of the group: consecutive ranks from the first marked entry */
-            int slot = slice_rank(sbits, spre, li0);
+            /* the patched ids of the group (src/sampler.c:21-52) */
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                if ((pb >> c) & 1u) xs[c] = L.pval[slot++];
+                if ((pb >> c) & 1u) xs[c] = hpatch(i0 + c);
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -393,7 +349,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     {
         const int idx[1] = {kPubMax};
-        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status, &misc[6]);
     }
     float M = -INFINITY;
     bool row_bad = false;
@@ -427,17 +383,19 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     tsum = wave_incl_scan_d(tsum);
     if (lane == 63) L.red[32 + wave_id()] = tsum;
     __syncthreads();
-    block_excl_scan(ce, nch, L.red);                        /* ce[c]: approximate e prefix at chunk c */
+    /* the slice's total is published first; the chunk prefix is built while
+     * the other slices' totals arrive */
     if (t == 0) {
         double e_tot = 0.0;
         for (int w2 = 0; w2 < T / 64; w2++) e_tot += L.red[32 + w2];
         at_st64(&mypub[kPubE], d2u(e_tot) | kReady);
     }
+    block_excl_scan(ce, nch, L.red);                        /* ce[c]: approximate e prefix at chunk c */
 
     /* ---- B: softmax normaliser ------------------------------------------ */
     {
         const int idx[1] = {kPubE};
-        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status, &misc[6]);
     }
     double Sapx = 0.0;
     for (int h = 0; h < G; h++) Sapx += u2d(pc[h * kPubWords + kPubE]);
@@ -501,7 +459,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             }
             {
                 const int idx[3] = {kPubS2, kPubA2, kPubN2};
-                row_gather<kLimit>(pubrow, G, idx, pc, p.status);
+                row_gather<kLimit>(pubrow, G, idx, pc, p.status, &misc[6]);
             }
             double S2 = 0.0, SA = 0.0;
             int64_t nkeep = 0;
@@ -549,7 +507,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
          *      and certifies them and hands them to the others ----------------- */
         {
             const int idx[2] = {kPubP, kPubP0};
-            row_gather<kLimit>(pubrow, G, idx, pc, p.status);
+            row_gather<kLimit>(pubrow, G, idx, pc, p.status, &misc[6]);
         }
         for (int h = 0; h < g; h++) RWg += u2d(pc[h * kPubWords + kPubP]);
         const double U = 0x1p-53;
@@ -673,7 +631,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 const uint64_t *src = &pubrow[hx * kPubWords + kPubX];
                 while (!((wv = at_ld64(src)) & kReady)) {
                     if (++spins > kLimit) {
-                        if (lane == 0 && p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
+                        if (lane == 0) {
+                            if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
+                            misc[6] = 1;
+                        }
                         wv = kReady | 0x7fffffffull;
                         break;
                     }
@@ -864,7 +825,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      *      exact start value (exact for slice 0: the sum starts at 0) ------- */
     {
         const int idx[1] = {kPubF};
-        row_gather<kLimit>(pubrow, G, idx, pc, p.status);
+        row_gather<kLimit>(pubrow, G, idx, pc, p.status, &misc[6]);
     }
     double Phat = 0.0;
     for (int h = 0; h < g; h++) Phat += u2d(pc[h * kPubWords + kPubF]);
@@ -1071,7 +1032,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         FullBase fb{&R};
         Scal Sc;
         int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
-        if (t == 0) p.out_ids[row] = pos;
+        /* after a wait gave up (the row is flagged invalid in the status word)
+         * the fallback may have run on an incomplete row maximum: the id stays
+         * inside the vocabulary */
+        if (t == 0) p.out_ids[row] = misc[6] && (pos < 0 || pos >= V) ? V - 1 : pos;
         for (int j = t; j < n_out; j += T) {
             int64_t o = (int64_t)row * n_out + j;
             float pj = fb.e(j) * Sc.inv;
@@ -1082,6 +1046,10 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
         }
     }
+    /* a wait of this workgroup gave up (the status word flags the launch): the
+     * row's workgroups may disagree on whether its sums were certified, so no
+     * workgroup may compose it; this one leaves an id inside the vocabulary */
+    if (misc[6] && t == 0) p.out_ids[row] = V - 1;
     row_exit(sync, pubrow, G);
 }
 

@@ -130,6 +130,36 @@ def test_long_history_vs_oracle(cuda, n_hist, k):
         assert_rows_match(w, res, list(range(w.rows)))
 
 
+@pytest.mark.parametrize("vocab,n_hist", [(32768, 1000), (151936, 1024), (151936, 700)])
+def test_fused_history_hash(cuda, vocab, n_hist):
+    """The fused full-vocabulary kernel's history table at its largest direct
+    history (up to 1,024 ids; longer ones are applied to a scratch copy first):
+    many repeats of few ids (long probe chains), ids on both sides of every
+    slice edge, all-distinct ids; both penalty orders.  Ids and rng states equal
+    the oracle's."""
+    rng = np.random.default_rng(vocab + n_hist)
+    w = W.c2(rows=4, vocab=vocab)
+    edges = [0, vocab - 1] + [e + d for e in range(4096, vocab, 4096) for d in (-1, 0)]
+    hist = []
+    for r in range(w.rows):
+        if r == 0:
+            h = rng.integers(0, vocab, n_hist)
+        elif r == 1:
+            h = rng.integers(0, 40, n_hist)                   # few distinct ids, many repeats
+        elif r == 2:
+            e = np.array(edges[:n_hist // 2])
+            h = np.concatenate([e, rng.integers(0, vocab, n_hist - len(e))])
+        else:
+            h = rng.permutation(vocab)[:n_hist]               # distinct ids
+        hist.append(h)
+    w.hist_off, w.hist_ids = W._csr(hist)
+    for order in (W.ORDER_NORTH_STAR, W.ORDER_REFERENCE):
+        w.order = order
+        _announce(f"fused history V={vocab} n={n_hist} order={order:#x}")
+        res = _batched(w, max_history=n_hist)
+        assert_rows_match(w, res, list(range(w.rows)))
+
+
 @pytest.mark.parametrize("path", [0, 1])
 def test_softcap_param_vs_oracle(cuda, path):
     """dlk_sample with softcap 30 on C5 rows (DFA mask, repetition penalty,
