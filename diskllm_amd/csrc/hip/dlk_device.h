@@ -171,4 +171,11 @@ DLK_DEV uint32_t wave_scan_sat_u32(uint32_t x, uint32_t cap) {
 
 }  // namespace dlk
 
+/* Branch hints for kernel code layout: a block behind DLK_COLD is taken rarely
+ * (or only on request) and is placed after the kernel's main path, which then
+ * stays contiguous and small enough for the instruction cache across launches;
+ * DLK_HOT marks the usual side of a branch. */
+#define DLK_COLD(c) __builtin_expect(!!(c), 0)
+#define DLK_HOT(c) __builtin_expect(!!(c), 1)
+
 #endif

@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     uint32_t mwd[EPT / 4];
     load_slice<EPT, 0, EPT / 4>(lg, mk, s0, s1, t, T, raw, mwd);
 
-    if (nh > p.plan.hcap || nh > T) {              /* (the host keeps both) */
+    if (DLK_COLD(nh > p.plan.hcap || nh > T)) {    /* (the host keeps both) */
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
             if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     if (g == 0 && t == 0) p.rng[row] = st;                  /* every workgroup has read it */
     const int n_out = p.n_out;
-    if (row_bad || !(M > -INFINITY)) {
+    if (DLK_COLD(row_bad || !(M > -INFINITY))) {
         /* every entry -inf, or a NaN / +inf entry: the softmax sum is NaN, no
          * comparison with it holds, and the draw falls through to index V-1 */
         if (g == 0) {
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         /* ---- p and the slice's p total (double, any order) ------------------ */
 #pragma unroll
         for (int j = 0; j < EPT; j++) v[j] = v[j] * inv;
-        if (g == 0 && n_out > 0 && (p.out_cand_ids || p.out_cand_probs)) {
+        if (DLK_COLD(g == 0 && n_out > 0 && (p.out_cand_ids || p.out_cand_probs))) {
 #pragma unroll
             for (int j = 0; j < EPT; j++) {
                 const int i = 4 * (t + (j / 4) * T) + (j & 3);
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
                 }
             }
         }
-        if (p.minp_on) {
+        if (DLK_COLD(p.minp_on)) {
             /* ---- B2: min-p (src/sampler.c:188-202): the entries with p >= min_p
              *      survive, in index order (none: every entry stays); their
              *      double sum, certified as inv is, gives inv2.  v becomes
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     /* (a uniform test first: the log must not be evaluated speculatively when
      * no log-probabilities are asked for) */
-    if (g == 0 && n_out > 0 && p.out_cand_logprobs) {
+    if (DLK_COLD(g == 0 && n_out > 0 && p.out_cand_logprobs)) {
 #pragma unroll
         for (int j = 0; j < EPT; j++) {
             const int i = 4 * (t + (j / 4) * T) + (j & 3);
@@ -1023,7 +1023,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     }
 
-    if (run_exact) {
+    if (DLK_COLD(run_exact)) {
         /* ---- exact fallback: one workgroup runs every sum sequentially-exact -- */
         int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
         Row R;

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         hist = p.hist_ids + p.hist_off[row];
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
-    if (nh > p.plan.hcap) {
+    if (DLK_COLD(nh > p.plan.hcap)) {
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
             if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
             ethr = asc_value(Km);
             exact_done = true;
         };
-        if (misc[8]) exact_pass();
+        if (DLK_COLD(misc[8])) exact_pass();
         /* ---- 4. candidates: the entries at or above the threshold -------- */
         bool all_groups = false, over = false;
         int C = 0;
@@ -573,8 +573,8 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
             __syncthreads();
             C = misc[10];
             over = (!all_groups && ng > f.grp_cap) || C > f.cand_cap;
-            if (over && !exact_done) exact_pass();  /* the row falls back: its maximum must be exact */
-            if (over || C >= f.KP || C >= nf) break;
+            if (DLK_COLD(over && !exact_done)) exact_pass();  /* the row falls back: its maximum must be exact */
+            if (DLK_HOT(over || C >= f.KP || C >= nf)) break;
             /* fewer than KP entries reach a threshold taken from raw logits
              * (penalties lowered some of them): the exact threshold, every group */
             if (!exact_done) exact_pass();
@@ -718,7 +718,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     const float r = rand_f32_from(st);
     if (t == 0) p.rng[row] = st;
     const int k = p.top_k;
-    if (irregular) {
+    if (DLK_COLD(irregular)) {
         /* NaN or +inf in the row: the reference's sequence on one thread */
         Row R;
         R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.pflag = L.pflag;
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         if (t == 0) emulate_topk_row(p, R, k, r, buf, row);
         return;
     }
-    if (NF == 0) {                           /* every entry -inf (see sampler_row.hip) */
+    if (DLK_COLD(NF == 0)) {                 /* every entry -inf (see sampler_row.hip) */
         if (t == 0) p.out_ids[row] = k - 1;
         out_cands_empty(NAN, NAN, true, k);
         return;
@@ -796,12 +796,12 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         }
         __syncthreads();
         int nsort = misc[46];
-        if (nsort > f.buf_cap) {
+        if (DLK_COLD(nsort > f.buf_cap)) {
             ok = false;
         } else {
             /* only the k best are sorted (k, plus any ties at the k-th s-key) */
             if (nsort > k + 16 && nsort <= T) nsort = keep_best(buf, nsort, k, &misc[48]);
-            if (nsort <= T) {
+            if (DLK_HOT(nsort <= T)) {
                 rank_sort_distinct(buf, nsort);
             } else {
                 int P = 64;
@@ -827,13 +827,13 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         }
     }
     __syncthreads();
-    if (!ok) {
+    if (DLK_COLD(!ok)) {
         /* exact selection over the whole row in this workgroup */
         int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
         R.np = np_row;
         uint32_t *hist2 = (uint32_t *)(buf + p.plan.kp);
         select_top_k(R, k, buf, p.plan.kp, hist2, L);
-    } else if (NF < k) {
+    } else if (DLK_COLD(NF < k)) {
         /* append the first k-NF -inf entries in index order */
         int need = k - NF, found = 0;
         int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
@@ -857,7 +857,7 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     R.maxv = cb.s(0);
     Scal S;
     int pos;
-    if (k <= 64) {
+    if (DLK_HOT(k <= 64)) {
         /* a few candidates: one wave runs the reference's loops literally */
         if (w == 0) {
             pos = pipeline_small(p, cb, k, r, S);
