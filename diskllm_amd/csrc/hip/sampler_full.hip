@@ -416,7 +416,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         /* ---- p and the slice's p total (double, any order) ------------------ */
 #pragma unroll
         for (int j = 0; j < EPT; j++) v[j] = v[j] * inv;
-        if (DLK_COLD(g == 0 && n_out > 0 && (p.out_cand_ids || p.out_cand_probs))) {
+        const bool want_cands = g == 0 && n_out > 0 && (p.out_cand_ids != nullptr || p.out_cand_probs != nullptr);
+        if (DLK_COLD(want_cands)) {
 #pragma unroll
             for (int j = 0; j < EPT; j++) {
                 const int i = 4 * (t + (j / 4) * T) + (j & 3);
@@ -661,7 +662,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     }
     /* (a uniform test first: the log must not be evaluated speculatively when
      * no log-probabilities are asked for) */
-    if (DLK_COLD(g == 0 && n_out > 0 && p.out_cand_logprobs)) {
+    const bool want_logp = g == 0 && n_out > 0 && p.out_cand_logprobs != nullptr;
+    if (DLK_COLD(want_logp)) {
 #pragma unroll
         for (int j = 0; j < EPT; j++) {
             const int i = 4 * (t + (j / 4) * T) + (j & 3);
