@@ -964,16 +964,52 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
         uint32_t cb = g > 0 ? wbase + (uint32_t)lane : 0u;
         int tok = -1;
-        for (int w = 0; w < nrng; w++) {
-            if (ballot(tok == -1) == 0) break;
-            if (tok != -1 || rbase[w] == kPastX) continue;
-            const uint32_t d = cb - rbase[w];
-            if (d >= 64u) {
-                tok = -2;
-            } else {
-                const int2 e = rres[w * 64 + (int)d];
-                if (e.y == -1) cb = (uint32_t)e.x;
-                else tok = e.y == -3 ? -2 : e.y;
+        if (g == 0) {
+            /* the row's first slice starts at exactly 0: every lane follows the
+             * same value, so the chain is uniform.  Every range's entries are
+             * loaded at once and each step reads its entry across lanes
+             * (v_readlane) instead of waiting on an LDS read per range: the
+             * first slice holds the draw's early binade changes, so it is the
+             * row's slowest and its chain of up to 16 dependent reads (about
+             * 2.3 us) was on the launch's critical path */
+            constexpr int kW = kFullThreads / 64;
+            int2 ent[kW];
+            uint32_t rbw[kW];
+#pragma unroll
+            for (int w = 0; w < kW; w++) {
+                ent[w] = w < nrng ? rres[w * 64 + lane] : make_int2(0, -2);
+                rbw[w] = w < nrng ? rbase[w] : kPastX;
+            }
+            uint32_t cu = 0;
+            int tu = -1;
+#pragma unroll
+            for (int w = 0; w < kW; w++) {
+                const uint32_t rb = (uint32_t)__builtin_amdgcn_readfirstlane((int)rbw[w]);
+                if (tu != -1 || w >= nrng || rb == kPastX) continue;
+                const uint32_t d = cu - rb;
+                if (d >= 64u) {
+                    tu = -2;
+                } else {
+                    const int ey = __builtin_amdgcn_readlane(ent[w].y, (int)d);
+                    const uint32_t ex = (uint32_t)__builtin_amdgcn_readlane(ent[w].x, (int)d);
+                    if (ey == -1) cu = ex;
+                    else tu = ey == -3 ? -2 : ey;
+                }
+            }
+            cb = cu;
+            tok = tu;
+        } else {
+            for (int w = 0; w < nrng; w++) {
+                if (ballot(tok == -1) == 0) break;
+                if (tok != -1 || rbase[w] == kPastX) continue;
+                const uint32_t d = cb - rbase[w];
+                if (d >= 64u) {
+                    tok = -2;
+                } else {
+                    const int2 e = rres[w * 64 + (int)d];
+                    if (e.y == -1) cb = (uint32_t)e.x;
+                    else tok = e.y == -3 ? -2 : e.y;
+                }
             }
         }
         uint64_t *lw = f.lanes + ((int64_t)row * G + g) * kLaneWords;
