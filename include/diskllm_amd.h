@@ -33,7 +33,8 @@ extern "C" {
 
 /* Device status bits written by the kernels (dlk_batch.status). */
 #define DLK_STATUS_HISTORY_TOO_LONG 1u  /* a row's history exceeded max_history: its id is -1 */
-#define DLK_STATUS_SYNC_TIMEOUT 2u      /* a cross-workgroup wait gave up (results of the call invalid) */
+#define DLK_STATUS_SYNC_TIMEOUT 2u      /* a cross-workgroup wait gave up: the call's ids are invalid,
+                                           though each stays inside [0, vocab) */
 #define DLK_STATUS_UNSUPPORTED_ROW 4u   /* a row whose s = (l - max) / T holds NaN with top_k > 4096: its id is -1 */
 
 /* Penalty ops, packed low nibble first into dlk_sample_params.penalty_order. */
