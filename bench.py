@@ -51,8 +51,9 @@ DOMINANT = {"C1": ("dlk::topk_kernel<false, false>", None),
 def profiled_traffic(kernel: str, tag: str = "full_kernel_c2"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
     profiles/<tag>_hbm_traffic.txt (FETCH_SIZE and WRITE_SIZE passes scaled by a
-    copy of known size), or None when the summary is absent or was taken on
-    another kernel."""
+    copy of known size), or None when the summary is absent, was taken on
+    another kernel, or on other library sources than the ones built here (its
+    "library source stamp:" line against diskllm_amd._lib.source_stamp())."""
     if tag is None:
         return None
     path = os.path.join(ROOT, "profiles", f"{tag}_hbm_traffic.txt")
@@ -62,6 +63,11 @@ def profiled_traffic(kernel: str, tag: str = "full_kernel_c2"):
         return None
     short = kernel.replace("dlk::", "")
     if short not in text:
+        return None
+    from diskllm_amd import _lib
+    stamp = _lib.source_stamp()
+    if not any(ln.startswith("library source stamp:") and ln.split(":", 1)[1].strip() == stamp
+               for ln in text.splitlines()):
         return None
     for ln in text.splitlines():
         if ln.startswith("scaled traffic per launch:"):
@@ -129,7 +135,7 @@ def run_other(name: str, args) -> int:
     with HIP events on the launch stream."""
     import numpy as np
     import torch
-    from diskllm_amd import api, workloads
+    from diskllm_amd import _lib, api, workloads
     from oracle import oracle as O
     dev = torch.device("cuda:0")
     w = workloads.CONFIGS[name]()
@@ -254,6 +260,7 @@ def run_other(name: str, args) -> int:
                    "vocab": w.vocab,
                    "parallelism": "none (1 GPU)"},
         "parity": parity,
+        "library_source_stamp": _lib.source_stamp(),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(kname, ktag),
                      "bytes_per_launch": nbytes, "ms_per_launch": round(ms_dev, 5), "kernel": kname},
@@ -498,6 +505,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batches", type=int, default=12,
+                    help="C2: distinct batches resident in HBM, one per step in turn (12 x 38.96 MB = 468 MB)")
     ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP", "CAP", "DROPIN"],
                     help="C2 (default) is the headline line; the others are the scope table's parity "
                          "configurations, measured the same way")
@@ -511,17 +520,9 @@ def main() -> int:
               "(row sharding) is not part of this build; run with --gpus 1", file=sys.stderr)
         return 2
 
-    maps_out = os.environ.get("DLK_EXIT_MAPS")
-    if maps_out:
-        # the process's mappings as the interpreter begins to exit, so that frames
-        # of a fault in a library's exit handler can be matched to their library
-        import atexit
-        import shutil
-        atexit.register(lambda: shutil.copyfile("/proc/self/maps", maps_out))
-
     import numpy as np
     import torch
-    from diskllm_amd import api, workloads
+    from diskllm_amd import _lib, api, workloads
     from oracle import oracle as O
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -539,33 +540,70 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"probe": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": args.steps}))
         return 0
-    w = workloads.c2()
-    db = api.to_device(w, device=dev)
+    # C2 over NB distinct batches resident at once (NB x 38.96 MB, past the
+    # 256 MB Infinity Cache), one batch per step in turn: every step reads fresh
+    # logits from HBM and meets its own rows' sums, as a decode loop does
+    NB = max(1, args.batches)
+    ws = [workloads.c2(seed=2 + 7919 * b) for b in range(NB)]
+    dbs = [api.to_device(w, device=dev) for w in ws]
+    w, db = ws[0], dbs[0]
     params = api.params_of(w)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
-    # parity of the benchmarked configuration (first step from the seeds)
-    api.sample(db, params, sh)
-    res = api.results(db)
-    orc = O.run_workload(w)
-    n_ok = int(np.sum(res["ids"] == orc["ids"]))
+    def parity_pass() -> tuple:
+        """One dlk_sample call per batch from its rows' current rng states,
+        checked against the oracle from the same states."""
+        ok = tot = 0
+        ids0 = None
+        for wb, d in zip(ws, dbs):
+            st = d.rng.cpu().numpy().view(np.uint64).copy()
+            api.sample(d, params, sh)
+            res = api.results(d)
+            if ids0 is None:
+                ids0 = res["ids"].copy()
+            for r in range(wb.rows):
+                ref = O.sample_row(O.prepared_row(wb, r), int(st[r]), wb.temperature, wb.top_k, wb.top_p,
+                                   wb.min_p)
+                ok += int(res["ids"][r] == ref["token"] and int(res["states"][r]) == ref["state"])
+                tot += 1
+        return ok, tot, ids0
 
-    run = api.sampler(db, params, sh)    # the call's structures built once: each step is the C call
-    for _ in range(args.warmup):
-        run()
+    n_ok0, n_tot0, first_ids = parity_pass()       # from the seeds
+    runs = [api.sampler(d, params, sh) for d in dbs]  # each call's structures built once
+    for i in range(args.warmup):
+        runs[i % NB]()
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        run()
-    ev1.record(stream)
+
+    def timed(seq) -> tuple:
+        """Wall clock and one event pair on the launch stream around len(seq) calls."""
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for f in seq:
+            f()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        return (t1 - t0) * 1e3 / len(seq), ev0.elapsed_time(ev1) / len(seq)
+
+    ms_step, ms_kernel = timed([runs[i % NB] for i in range(args.steps)])
+    ms_step_fixed, ms_kernel_fixed = timed([runs[0]] * args.steps)
+    # per-launch spread: one event before each call, so consecutive events bracket
+    # one launch (each interval also holds one event record)
+    nl = min(args.steps, 2000)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(nl + 1)]
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    ms_kernel = ev0.elapsed_time(ev1) / args.steps
+    for i in range(nl):
+        evs[i].record(stream)
+        runs[i % NB]()
+    evs[nl].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(nl)], np.float64)
+    # parity again after the timed steps: every row's rng state has moved on
+    n_ok1, n_tot1, _ = parity_pass()
     bytes_launch = BYTES_PER_ROW * ROWS
     achieved = bytes_launch / (ms_kernel * 1e-3) / 1e9
     rows_s = ROWS / (ms_step * 1e-3)
@@ -585,15 +623,30 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "C2: batch-64 full-vocab nucleus sampling, fp32 logits [64,151936], rep 1.15 / "
                                "freq 0.3 / pres 0.5 over 256-id Zipf history, T 1.0, top-p 0.9, no top-k",
-                   "rows": ROWS, "vocab": VOCAB, "history": HIST, "parallelism": "none (1 GPU)"},
+                   "rows": ROWS, "vocab": VOCAB, "history": HIST, "parallelism": "none (1 GPU)",
+                   "batches": NB, "resident_bytes": NB * bytes_launch,
+                   "step": f"one dlk_sample call on batch (step mod {NB}): {NB} distinct C2 batches "
+                           f"(seeds 2 + 7919 b) resident in HBM, {NB * bytes_launch / 1e6:.0f} MB, "
+                           f"past the 256 MB Infinity Cache"},
         "hbm_gbps": round(bytes_launch / (ms_step * 1e-3) / 1e9, 1),
         "hbm_frac": round(bytes_launch / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "parity": f"{n_ok}/{ROWS} token ids bit-identical to the oracle",
+        "parity": f"{n_ok0}/{n_tot0} token ids and rng states bit-identical to the oracle from the seeds, "
+                  f"{n_ok1}/{n_tot1} after the timed steps ({NB} batches)",
         "roofline": {"bound": "hbm", "kernel": fused_kernel_name(ROWS, VOCAB), "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": profiled_traffic(fused_kernel_name(ROWS, VOCAB)), "bytes_per_launch": bytes_launch, "ms_per_launch": round(ms_kernel, 5)},
+                     "traffic": profiled_traffic(fused_kernel_name(ROWS, VOCAB)), "bytes_per_launch": bytes_launch,
+                     "ms_per_launch": round(ms_kernel, 5)},
+        "library_source_stamp": _lib.source_stamp(),
+        "launch_spread": {"n": nl, "mean_ms": round(float(per.mean()), 5),
+                          "p50_ms": round(float(np.percentile(per, 50)), 5),
+                          "p99_ms": round(float(np.percentile(per, 99)), 5), "max_ms": round(float(per.max()), 5),
+                          "note": "an event before each launch; each interval holds one event record"},
+        "fixed_batch": {"ms_per_step": round(ms_step_fixed, 5), "ms_per_launch": round(ms_kernel_fixed, 5),
+                        "value": round(ROWS / (ms_step_fixed * 1e-3), 1),
+                        "note": "batch 0 every step (39 MB, inside the Infinity Cache)"},
         "cpu_baseline": None,
     }
+    res = {"ids": first_ids}
     if not args.no_cpu:
         nthreads = host_threads()
         cb = cpu_baseline(w, args.cpu_runs, nthreads)

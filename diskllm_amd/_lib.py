@@ -76,7 +76,7 @@ class CsrVocab(C.Structure):
 # Every symbol the public headers declare (checked by the CPU test suite).
 EXPORTS = [
     # include/diskllm_amd.h
-    "dlk_seed_state", "dlk_sample", "dlk_sample_noalloc", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
+    "dlk_seed_state", "dlk_sample", "dlk_sample_noalloc", "dlk_release_stream", "dlk_dfa_mask", "dlk_expf", "dlk_apply_penalties", "dlk_grammar_mode_of",
     "dlk_grammar_row_init", "dlk_grammar_row_feed", "dlk_grammar_mask", "dlk_grammar_advance", "dlk_sample_grammar",
     "dlk_vocab_csr_from_gguf", "dlk_csr_token_str", "dlk_softcap",
     # include/sampler.h
@@ -87,6 +87,27 @@ EXPORTS = [
     "diskllm_grammar_free", "diskllm_grammar_reset", "diskllm_grammar_accept_str", "diskllm_grammar_advance",
     "diskllm_grammar_is_finished", "diskllm_grammar_apply_mask",
 ]
+
+
+def source_stamp() -> str:
+    """First 16 hex digits of a SHA-256 over the library's sources (csrc/hip,
+    csrc/host, the Makefile, the export map and include/*.h, by relative path
+    and content): the build a measurement was taken on.  Committed profile
+    summaries record it, so a figure is only reused for the sources it measured."""
+    import glob
+    import hashlib
+    h = hashlib.sha256()
+    root = os.path.dirname(HERE)
+    files = sorted(glob.glob(os.path.join(CSRC, "hip", "*")) + glob.glob(os.path.join(CSRC, "host", "*")) +
+                   [os.path.join(CSRC, "Makefile"), os.path.join(CSRC, "exports.map")] +
+                   glob.glob(os.path.join(root, "include", "*.h")))
+    for f in files:
+        if os.path.isfile(f):
+            h.update(os.path.relpath(f, root).encode() + b"\0")
+            with open(f, "rb") as fh:
+                h.update(fh.read())
+            h.update(b"\0")
+    return h.hexdigest()[:16]
 
 
 def build(quiet: bool = True) -> None:
@@ -115,6 +136,8 @@ def lib() -> C.CDLL:
         L.dlk_sample.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p]
         L.dlk_sample_noalloc.restype = C.c_int
         L.dlk_sample_noalloc.argtypes = [C.POINTER(Batch), C.c_int, C.c_int, C.POINTER(SampleParams), C.c_void_p]
+        L.dlk_release_stream.restype = C.c_int
+        L.dlk_release_stream.argtypes = [C.c_void_p]
         L.dlk_dfa_mask.restype = C.c_int
         L.dlk_dfa_mask.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                    C.c_int, C.c_uint64, C.c_void_p, C.c_int64, C.c_void_p]

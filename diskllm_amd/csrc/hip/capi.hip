@@ -21,6 +21,12 @@ extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, size_t
 extern "C" int dlk_topk_kernel_occupancy(int kind, size_t lds);
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
 extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap);
+extern "C" int dlk_launch_long_history_penalties(float *logits, int64_t ld, int rows, int vocab,
+                                                 const int32_t *hist_off, const int32_t *hist_ids, uint32_t order,
+                                                 float rep, float freq, float pres, int max_hist, int32_t *too_long,
+                                                 const uint64_t *rng, uint64_t *rng_saved, hipStream_t stream);
+extern "C" int dlk_launch_long_history_fixup(int rows, const int32_t *too_long, const uint64_t *rng_saved,
+                                             uint64_t *rng, int32_t *out_ids, uint32_t *status, hipStream_t stream);
 extern "C" int dlk_launch_prepare_rows(const float *src, int64_t ld, float *dst, int64_t dld, int rows, int vocab,
                                        const uint32_t *mask, int64_t mask_ld, const int32_t *mask_row, float cap,
                                        hipStream_t stream);
@@ -226,13 +232,18 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     if (dev < 0 || dev >= 64) return DLK_ERR_HIP;
     if (!n_cu[dev] && hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return DLK_ERR_HIP;
+    /* occupancy per (device, kind, LDS): a fixed table, so that no call
+     * allocates host memory either (past its size a query is simply repeated) */
     struct Occ { int dev, kind; size_t lds; int n; };
-    static std::vector<Occ> occ_cache;
+    static Occ occ_cache[256];
+    static int n_occ = 0;
     auto resident = [&](size_t lds) {
-        for (const auto &e : occ_cache)
+        for (int i = 0; i < n_occ; i++) {
+            const Occ &e = occ_cache[i];
             if (e.dev == dev && e.kind == kind && e.lds == lds) return e.n * n_cu[dev];
+        }
         const int n = dlk_topk_kernel_occupancy(kind, lds);
-        occ_cache.push_back(Occ{dev, kind, lds, n});
+        if (n_occ < 256) occ_cache[n_occ++] = Occ{dev, kind, lds, n};
         return n * n_cu[dev];
     };
     auto slice_of = [&](int g) { return ((vocab + g - 1) / g + unit - 1) / unit * unit; };
@@ -304,15 +315,18 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     if (lds > kMaxLds) return 1;
     /* resident workgroups of this instance: queried once per (device, ept, LDS) */
     struct CapEntry { int dev, ept; size_t lds; int softcap, cap; };
-    static std::vector<CapEntry> cap_cache;
+    static CapEntry cap_cache[256];       /* fixed, as occ_cache above */
+    static int n_cap = 0;
     const int softcap = p.cap > 0.0f ? 1 : 0;
     int dev = 0, cap = -1;
     if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
-    for (const auto &e : cap_cache)
+    for (int i = 0; i < n_cap; i++) {
+        const CapEntry &e = cap_cache[i];
         if (e.dev == dev && e.ept == ept && e.lds == lds && e.softcap == softcap) { cap = e.cap; break; }
+    }
     if (cap < 0) {
         cap = dlk_full_kernel_capacity(ept, lds, softcap);
-        cap_cache.push_back(CapEntry{dev, ept, lds, softcap, cap});
+        if (n_cap < 256) cap_cache[n_cap++] = CapEntry{dev, ept, lds, softcap, cap};
     }
     int rows_per = cap / G;
     if (rows_per < 1) return 1;
@@ -378,21 +392,26 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
     if (b->hist_off && pow2_at_least(max_hist, 64) > kHcapDirect) {
         /* a history too long to stage in LDS: the rows as sampler_sample would
          * see them -- soft-cap, mask, penalties (src/core/sampler_api.c:51-61) --
-         * in a scratch copy; then the sampling alone over the copy */
+         * in a scratch copy; then the sampling alone over the copy.  A row whose
+         * history exceeds max_history is flagged by the penalty pass (its rng
+         * state kept) and given id -1 and the status bit after the sampling,
+         * as the sampling kernels do for the histories they stage */
         if (rows > 65535) return DLK_ERR_UNSUPPORTED;
         const int64_t ldp = ((int64_t)vocab + 63) & ~(int64_t)63;
+        const size_t prep_b = r16((size_t)rows * ldp * 4), flag_b = r16((size_t)rows * 4);
         WsView ws;
-        if (!workspace(stream, 1, 0, (size_t)rows * ldp * 4, ws)) return g_ws_err;
+        if (!workspace(stream, 1, 0, prep_b + flag_b + (size_t)rows * 8, ws)) return g_ws_err;
         float *prep = (float *)ws.data;
+        int32_t *too_long = (int32_t *)(ws.data + prep_b);
+        uint64_t *rng_saved = (uint64_t *)(ws.data + prep_b + flag_b);
         if (dlk_launch_prepare_rows(b->logits, b->ld, prep, ldp, rows, vocab, b->mask, b->mask_ld, b->mask_row,
                                     cap_on ? prm->softcap : 0.0f, stream) != 0)
             return DLK_ERR_HIP;
-        if (b->hist_off) {
-            const int rc = dlk_apply_penalties(prep, ldp, rows, vocab, b->hist_off, b->hist_ids, prm->penalty_order,
-                                               prm->repeat_penalty, prm->frequency_penalty, prm->presence_penalty,
-                                               stream);
-            if (rc != DLK_OK) return rc;
-        }
+        int rc = dlk_launch_long_history_penalties(prep, ldp, rows, vocab, b->hist_off, b->hist_ids,
+                                                   prm->penalty_order, prm->repeat_penalty, prm->frequency_penalty,
+                                                   prm->presence_penalty, max_hist, too_long,
+                                                   greedy ? nullptr : b->rng, rng_saved, stream);
+        if (rc != DLK_OK) return rc;
         dlk_batch b2 = *b;
         b2.logits = prep;
         b2.ld = ldp;
@@ -403,7 +422,10 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
         dlk_sample_params p2 = *prm;
         p2.softcap = 0.0f;
         p2.max_history = 0;
-        return sample_impl(&b2, rows, vocab, &p2, stream);
+        rc = sample_impl(&b2, rows, vocab, &p2, stream);
+        if (rc != DLK_OK) return rc;
+        return dlk_launch_long_history_fixup(rows, too_long, rng_saved, greedy ? nullptr : b->rng, b->out_ids,
+                                             b->status, stream);
     }
 
     dlk::RowParams p;
@@ -471,21 +493,27 @@ extern "C" int dlk_sample(const dlk_batch *b, int rows, int vocab, const dlk_sam
     return sample_impl(b, rows, vocab, prm, stream);
 }
 
-/* Frees the workspace buffers of `stream` on the current device (the drop-ins
- * call it before they destroy a stream).  Not exported. */
-extern "C" void dlk_internal_release_stream(hipStream_t stream) {
+/* Frees the workspace buffers of `stream` on the current device, after the
+ * stream's queued work has finished with them (include/diskllm_amd.h). */
+extern "C" int dlk_release_stream(hipStream_t stream) {
     std::lock_guard<std::mutex> lock(g_mu);
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return;
+    if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
+    int rc = DLK_OK;
+    bool synced = false;
     for (size_t i = 0; i < g_ws.size();) {
         if (g_ws[i].dev == dev && g_ws[i].stream == stream) {
-            (void)hipStreamSynchronize(stream);
-            (void)hipFree(g_ws[i].ptr);
+            if (!synced) {
+                if (hipStreamSynchronize(stream) != hipSuccess) rc = DLK_ERR_HIP;
+                synced = true;
+            }
+            if (g_ws[i].ptr && hipFree(g_ws[i].ptr) != hipSuccess) rc = DLK_ERR_HIP;
             g_ws.erase(g_ws.begin() + (long)i);
         } else {
             i++;
         }
     }
+    return rc;
 }
 
 /* dlk_sample with its workspace in the fixed per-device scratch array: no

@@ -4,6 +4,7 @@
 #include <pthread.h>
 #include <string.h>
 
+#include "diskllm_amd.h"
 #include "dropin.h"
 
 int dlk_dropin_init(dlk_dropin_ctx *c) {
@@ -19,12 +20,10 @@ fail:
     return -1;
 }
 
-void dlk_internal_release_stream(hipStream_t stream);   /* capi.hip: the stream's workspace */
-
 void dlk_dropin_release(dlk_dropin_ctx *c) {
     if (c->stream) {
         hipStreamSynchronize(c->stream);
-        dlk_internal_release_stream(c->stream);
+        (void)dlk_release_stream(c->stream);
     }
     hipFree(c->logits);
     hipFree(c->hist);

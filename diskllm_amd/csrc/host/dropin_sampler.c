@@ -3,6 +3,7 @@
  * host API (include/sampler.h:19-34, src/sampler.c) as copies around the
  * batched entry points of diskllm_amd.h.
  */
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -13,6 +14,7 @@
 struct sampler {
     sampler_config cfg;
     uint64_t rng;            /* host copy of the xorshift state (src/sampler.c:63) */
+    int path;                /* DLK_PATH_* of the first attempt (DLK_DROPIN_PATH, tests) */
     dlk_dropin_ctx dev;
 };
 
@@ -22,6 +24,10 @@ sampler *sampler_create(const sampler_config *cfg) {
     if (!s) return NULL;
     s->cfg = *cfg;
     s->rng = dlk_seed_state(cfg->seed);                      /* src/sampler.c:87 */
+    /* test hook: the implementation the first attempt of each draw uses (e.g.
+     * DLK_PATH_FULL_NO_WAIT to force the sync-timeout recovery below) */
+    const char *ps = getenv("DLK_DROPIN_PATH");
+    s->path = ps ? atoi(ps) : DLK_PATH_AUTO;
     if (dlk_dropin_init(&s->dev) != 0) {
         free(s);
         return NULL;
@@ -35,9 +41,33 @@ void sampler_free(sampler *s) {
     free(s);
 }
 
-/* One row through dlk_sample on `c`; rng updated in place when not greedy. */
+/* A device failure the reference API has no channel for: said once on stderr. */
+static void report_device_failure(const char *what) {
+    static int said;
+    if (!said) {
+        said = 1;
+        fprintf(stderr, "libdiskllm_amd: %s could not reach the GPU; continuing as the reference does "
+                        "without its resources (src/sampler.c:145-147)\n", what);
+    }
+}
+
+/* The reference's greedy_sample (src/sampler.c:9-19) on the host row: the
+ * answer of sampler_sample and greedy_sample when the device cannot be reached,
+ * as the reference degrades to greedy when it cannot get its work buffer
+ * (src/sampler.c:145-147, no random number drawn). */
+static int host_greedy(const float *logits, int vocab) {
+    int best = 0;
+    float bv = logits[0];
+    for (int i = 1; i < vocab; i++)
+        if (logits[i] > bv) { bv = logits[i]; best = i; }
+    return best;
+}
+
+/* One row through dlk_sample on `c` with the rng state *rng; on success the
+ * token, the status word in *status and the advanced state in *rng_out (not
+ * greedy); -1 when a device call fails. */
 static int sample_one(dlk_dropin_ctx *c, const float *logits, int vocab, float temperature, int top_k, float top_p,
-                      float min_p, uint64_t *rng) {
+                      float min_p, int path, const uint64_t *rng, uint64_t *rng_out, uint32_t *status) {
     if (dlk_dropin_reserve(c, vocab, 0) != 0) return -1;
     const int greedy = temperature == 0.0f;
     if (hipMemcpyAsync(c->logits, logits, (size_t)vocab * sizeof(float), hipMemcpyHostToDevice, c->stream) !=
@@ -60,6 +90,7 @@ static int sample_one(dlk_dropin_ctx *c, const float *logits, int vocab, float t
     p.top_p = top_p;
     p.min_p = min_p;
     p.repeat_penalty = 1.0f;
+    p.path = path;
     if (hipMemsetAsync(c->status, 0, sizeof(uint32_t), c->stream) != hipSuccess) return -1;
     if (dlk_sample(&b, 1, vocab, &p, c->stream) != DLK_OK) return -1;
     int32_t id = -1;
@@ -69,24 +100,54 @@ static int sample_one(dlk_dropin_ctx *c, const float *logits, int vocab, float t
     uint64_t r = 0;
     if (!greedy && hipMemcpyAsync(&r, c->rng, sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream) != hipSuccess)
         return -1;
-    if (hipStreamSynchronize(c->stream) != hipSuccess || st != 0) return -1;
-    if (!greedy) *rng = r;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return -1;
+    *status = st;
+    if (!greedy) *rng_out = r;
     return id;
 }
 
+/* The reference always returns a token (src/sampler.c:136-234): its caller
+ * feeds it straight to the next decode step (src/cli/main.c:386-388).  A
+ * launch whose cross-workgroup wait gave up (another kernel holding the GPU)
+ * is run again on the row kernel, which has no such waits, from the same rng
+ * state, so the token and the state are the reference's; if the device
+ * cannot be reached at all the row is sampled greedily on the host, without
+ * drawing, as the reference does when it has no work buffer. */
 int sampler_sample(sampler *s, float *logits, int vocab_size) {
     if (!s || !logits || vocab_size <= 0) return -1;
-    return sample_one(&s->dev, logits, vocab_size, s->cfg.temperature, s->cfg.top_k, s->cfg.top_p, s->cfg.min_p,
-                      &s->rng);
+    const sampler_config *cf = &s->cfg;
+    uint64_t next = s->rng;
+    uint32_t st = 0;
+    int id = sample_one(&s->dev, logits, vocab_size, cf->temperature, cf->top_k, cf->top_p, cf->min_p, s->path,
+                        &s->rng, &next, &st);
+    if (id >= 0 && (st & DLK_STATUS_SYNC_TIMEOUT)) {
+        st = 0;
+        id = sample_one(&s->dev, logits, vocab_size, cf->temperature, cf->top_k, cf->top_p, cf->min_p, DLK_PATH_ROW,
+                        &s->rng, &next, &st);
+    }
+    if (id < 0 || st != 0 || id >= vocab_size) {
+        report_device_failure("sampler_sample");
+        return host_greedy(logits, vocab_size);
+    }
+    if (cf->temperature != 0.0f) s->rng = next;
+    return id;
 }
 
 int greedy_sample(const float *logits, int vocab_size) {
     if (!logits || vocab_size <= 0) return 0;
     dlk_dropin_ctx *c = dlk_dropin_shared_lock();
-    if (!c) return -1;
-    uint64_t unused = 1;
-    const int id = sample_one(c, logits, vocab_size, 0.0f, 0, 1.0f, 0.0f, &unused);
-    dlk_dropin_shared_unlock();
+    int id = -1;
+    uint32_t st = 0;
+    if (c) {
+        const uint64_t unused = 1;
+        uint64_t out = 1;
+        id = sample_one(c, logits, vocab_size, 0.0f, 0, 1.0f, 0.0f, DLK_PATH_AUTO, &unused, &out, &st);
+        dlk_dropin_shared_unlock();
+    }
+    if (id < 0 || st != 0 || id >= vocab_size) {
+        report_device_failure("greedy_sample");
+        return host_greedy(logits, vocab_size);
+    }
     return id;
 }
 
@@ -104,6 +165,11 @@ static int cmp_id_pos(const void *a, const void *b) {
     const id_pos *x = (const id_pos *)a, *y = (const id_pos *)b;
     if (x->id != y->id) return x->id < y->id ? -1 : 1;
     return x->pos < y->pos ? -1 : x->pos > y->pos;
+}
+
+static void report_penalty_failure(uint32_t op) {
+    fprintf(stderr, "libdiskllm_amd: sampler_apply_%s_penalty could not reach the GPU; the row was not "
+                    "penalised\n", op == DLK_OP_REPETITION ? "repetition" : "presence");
 }
 
 static void penalty_one(float *logits, int vocab, const int *seen, int n, uint32_t op, float value) {
@@ -125,6 +191,7 @@ static void penalty_one(float *logits, int vocab, const int *seen, int n, uint32
             slots[j] = nd - 1;
         }
     }
+    int done = nd == 0 && (ip && slots && ids && vals);
     dlk_dropin_ctx *c = nd ? dlk_dropin_shared_lock() : NULL;
     if (c) {
         if (dlk_dropin_reserve(c, nd, m) == 0) {
@@ -139,11 +206,17 @@ static void penalty_one(float *logits, int vocab, const int *seen, int n, uint32
                                          op == DLK_OP_REPETITION ? value : 1.0f, 0.0f,
                                          op == DLK_OP_PRESENCE ? value : 0.0f, c->stream) == DLK_OK;
             if (ok) ok = hipMemcpyAsync(vals, c->logits, bytes, hipMemcpyDeviceToHost, c->stream) == hipSuccess;
-            if (hipStreamSynchronize(c->stream) == hipSuccess && ok)
+            if (hipStreamSynchronize(c->stream) == hipSuccess && ok) {
                 for (int d = 0; d < nd; d++) logits[ids[d]] = vals[d];
+                done = 1;
+            }
         }
         dlk_dropin_shared_unlock();
     }
+    /* the reference's penalties cannot fail (src/sampler.c:21-52); these can
+     * only when host or device memory runs out or the GPU is gone: said on
+     * stderr rather than passed over in silence */
+    if (!done) report_penalty_failure(op);
     free(ip);
     free(slots);
     free(ids);

@@ -100,6 +100,17 @@ uint64_t dlk_seed_state(uint64_t seed);
 int dlk_sample(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
                hipStream_t stream);
 
+/* Workspace lifetime.  dlk_sample and the calls built on it keep one lazily
+ * grown device workspace per (device, stream) they are called on (kernels queued
+ * on one stream run in order and share it; calls on different streams never
+ * do).  It is held until the process ends or until this call, which waits for
+ * the stream's queued work and frees the stream's workspaces on the current
+ * device.  Call it before destroying a stream that was passed to dlk_sample; a
+ * later call on the stream allocates afresh.  No counterpart in the reference,
+ * whose sampler owns a host work buffer freed by sampler_free
+ * (src/sampler.c:91-95). */
+int dlk_release_stream(hipStream_t stream);
+
 /* dlk_sample without any allocation.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops and harnesses that forbid hipMalloc).  Same arguments, kernels

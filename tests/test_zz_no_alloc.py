@@ -96,3 +96,39 @@ def test_noalloc_refuses_what_needs_more(cuda):
     prm = api.params_of(w, max_history=5000)
     _announce("noalloc refuses max_history 5000")
     assert _call("dlk_sample_noalloc", db, prm) == _lib.DLK_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("make,rows", [(W.c2, 16), (W.c3, 8)], ids=["full", "topk"])
+def test_noalloc_allocates_nothing_and_captures(cuda, make, rows):
+    """Device free memory is unchanged across a dlk_sample_noalloc call, and the
+    call captured into a HIP graph (torch.cuda.graph; the counters are cleared by
+    a fill kernel, not a memset node) gives, on each of four replays with eager
+    work and synchronisation between them, the ids and rng states dlk_sample
+    gives for the same step.  The first call of a shape (outside the capture)
+    fills the host-side occupancy tables."""
+    import torch
+    from diskllm_amd import api
+    w = make(rows=rows)
+    a, b = api.to_device(w), api.to_device(w)
+    prm = api.params_of(w)
+    _announce(f"noalloc {w.name} rows={rows}: warm-up, memory")
+    assert _call("dlk_sample_noalloc", a, prm) == _lib.DLK_OK       # warm-up (host tables)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert _call("dlk_sample_noalloc", a, prm) == _lib.DLK_OK
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    a.reset_rng()
+    g = torch.cuda.CUDAGraph()
+    _announce(f"noalloc {w.name} rows={rows}: capture")
+    with torch.cuda.graph(g):
+        rc = _call("dlk_sample_noalloc", a, prm)
+    assert rc == _lib.DLK_OK
+    for rep in range(4):
+        _announce(f"noalloc {w.name} rows={rows}: replay {rep}")
+        g.replay()
+        torch.cuda.synchronize()
+        ra = api.results(a)
+        assert _call("dlk_sample", b, prm) == _lib.DLK_OK
+        rb = api.results(b)
+        _same(ra, rb)
