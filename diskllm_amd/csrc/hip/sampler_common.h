@@ -335,8 +335,9 @@ struct KthKey {
     uint32_t key;
     int below, equal;
 };
-__device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist, Lds &L) {
-    const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id();
+template <class KeyFn>
+__device__ __forceinline__ KthKey radix_kth_keys(KeyFn key_of, int V, int k, uint32_t *hist, Lds &L) {
+    const int t = threadIdx.x, T = blockDim.x, lane = lane_id();
     uint32_t prefix = 0;
     int krem = k, below_total = 0, eq_count = 0;
     for (int rd = 0; rd < 3; rd++) {
@@ -347,7 +348,7 @@ __device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist,
         for (int b = t; b < nb; b += T) hist[b] = 0;
         __syncthreads();
         for (int i = t; i < V; i += T) {
-            uint32_t key = desc_key(scaled(R, i));
+            uint32_t key = key_of(i);
             bool in = rd == 0 || (key >> hsh) == prefix;
             if (in) atomicAdd(&hist[(key >> sh) & (nb - 1)], 1u);
         }
@@ -383,6 +384,43 @@ __device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist,
         below_total += below;
     }
     return KthKey{prefix, below_total, eq_count};
+}
+
+__device__ __forceinline__ KthKey radix_kth(const Row &R, int k, uint32_t *hist, Lds &L) {
+    return radix_kth_keys([&](int i) { return desc_key(scaled(R, i)); }, R.V, k, hist, L);
+}
+
+/* desc_key with every NaN last (key 0xffffffff, past -inf): the order the
+ * reference's top-k gives the entries it can take when no NaN sits among the
+ * first k (a NaN past them never enters, src/sampler.c:122). */
+DLK_DEV uint32_t key_nan_last(float s) { return s != s ? 0xffffffffu : desc_key(s); }
+
+/* Index of the need-th (1-based) element i < V, in index order, with
+ * key_of(i) == key; the block's count of such elements must reach need. */
+template <class KeyFn>
+__device__ __forceinline__ int nth_index_with_key(KeyFn key_of, int V, uint32_t key, int need, Lds &L) {
+    const int t = threadIdx.x, T = blockDim.x, lane = lane_id();
+    int *wcnt = (int *)L.red;
+    int taken = 0, found = -1;
+    for (int i0 = 0; i0 < V && found < 0; i0 += T) {
+        const int i = i0 + t;
+        const bool hit = i < V && key_of(i) == key;
+        const uint64_t bal = ballot(hit);
+        if (lane == 0) wcnt[wave_id()] = __popcll(bal);
+        __syncthreads();
+        int before = 0, tot = 0;
+        for (int w = 0; w < n_waves(); w++) {
+            if (w < wave_id()) before += wcnt[w];
+            tot += wcnt[w];
+        }
+        const int rank = taken + before + __popcll(bal & ((1ull << lane) - 1));
+        if (hit && rank == need - 1) L.bi[12] = i;
+        taken += tot;
+        __syncthreads();
+        if (taken >= need) found = L.bi[12];
+        __syncthreads();
+    }
+    return found;
 }
 
 /* First k elements under (s desc, index asc), sorted, into cand[0..k) as
@@ -463,14 +501,15 @@ constexpr int kLsdWords = 256 + 16 * 256 + 16;
 __device__ __forceinline__ void select_top_k_global(const Row &R, int k, uint64_t *a, uint64_t *b, uint32_t *hist,
                                                     uint32_t *lsd, Lds &L) {
     const int t = threadIdx.x, T = blockDim.x, V = R.V, lane = lane_id(), w = wave_id(), nw = n_waves();
-    const KthKey kk = radix_kth(R, k, hist, L);
+    /* (NaN keys last: a row reaching here holds no NaN among its first k) */
+    const KthKey kk = radix_kth_keys([&](int i) { return key_nan_last(scaled(R, i)); }, V, k, hist, L);
     const int need = k - kk.below;                 /* ties at the k-th key to take, >= 1 */
     uint32_t *red = lsd + 256 + 16 * 256;
     /* ---- collection in index order: a tile of T elements at a time -------- */
     int base_lt = 0, base_tie = 0;
     for (int i0 = 0; i0 < V; i0 += T) {
         const int i = i0 + t;
-        const uint32_t key = i < V ? desc_key(scaled(R, i)) : 0xffffffffu;
+        const uint32_t key = i < V ? key_nan_last(scaled(R, i)) : 0xffffffffu;
         const bool lt = i < V && key < kk.key, tie = i < V && key == kk.key;
         const uint32_t v = (lt ? 1u : 0u) | (tie ? 0x10000u : 0u);
         uint32_t tot = 0;

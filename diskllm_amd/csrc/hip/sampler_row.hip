@@ -100,20 +100,49 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
     if (snan && p.topk_on && (k <= kEmulateMaxK || bv > -INFINITY)) {
         if (k <= kEmulateMaxK) {
             if (t == 0) emulate_topk_row(p, R, k, r, (uint64_t *)L.region, row);
-        } else {
-            /* the reference's insertion sort with NaN keys, O(V k) on one thread,
-             * is not run for large k */
-            if (t == 0) {
-                p.out_ids[row] = -1;
-                if (p.status) atomicOr(p.status, DLK_STATUS_UNSUPPORTED_ROW);
+            return;
+        }
+        /* k too large for the one-thread emulation: the reference's insertion
+         * sort with NaN keys in closed form (src/sampler.c:109-134).  A NaN never
+         * moves (every comparison with it is false) and stops any element moving
+         * past it, and no entry past the first k replaces a NaN at k-1 or enters
+         * as a NaN.  So with q the last NaN among the first k: if q = k-1 the
+         * buffer ends with it; otherwise the entries after q form a window that
+         * ends up holding the best k-1-q entries, under (s desc, index asc), of
+         * the window's own entries and the non-NaN entries past k.  Any NaN among
+         * the first k makes the softmax sum NaN, every comparison of the draw
+         * false, and the draw falls through to buf[k-1] (:226-233).  With no NaN
+         * among the first k the NaN entries never enter and the ordinary path
+         * below selects among the others (NaN keys last). */
+        R.M = first_nan ? NAN : bv;               /* the reference's max loop (:155-158) */
+        int q = -1;
+        for (int i = t; i < k; i += blockDim.x)
+            if (isnan(scaled(R, i))) q = i;
+        for (int m = 32; m >= 1; m >>= 1) q = max(q, shfl_xor(q, m));
+        if (lane == 0) L.bi[32 + wave_id()] = q;
+        __syncthreads();
+        for (int w2 = 0; w2 < n_waves(); w2++) q = max(q, L.bi[32 + w2]);
+        __syncthreads();
+        if (q >= 0) {
+            int tok = k - 1;
+            if (q < k - 1) {
+                const int win = k - 1 - q;
+                auto key_of = [&](int i) {
+                    const float s = scaled(R, i);
+                    return (i <= q || s != s) ? 0xffffffffu : desc_key(s);
+                };
+                const KthKey kk = radix_kth_keys(key_of, V, win, (uint32_t *)L.region, L);
+                tok = nth_index_with_key(key_of, V, kk.key, win - kk.below, L);
             }
+            if (t == 0) p.out_ids[row] = tok;
+            /* every probability is NaN; the buffer order is not produced */
             for (int j = t; j < n_out; j += blockDim.x) {
                 if (p.out_cand_ids) p.out_cand_ids[(int64_t)row * n_out + j] = -1;
                 if (p.out_cand_probs) p.out_cand_probs[(int64_t)row * n_out + j] = NAN;
                 if (p.out_cand_logprobs) p.out_cand_logprobs[(int64_t)row * n_out + j] = NAN;
             }
+            return;
         }
-        return;
     }
     if (((snan || spinf) && !p.topk_on) || !(bv > -INFINITY)) {
         /* without top-k a NaN or +inf entry of s makes the softmax sum NaN (+inf -
@@ -148,9 +177,10 @@ __global__ __launch_bounds__(1024) void row_kernel(RowParams p) {
         }
         CandBase cb{&R, cand};
         R.maxv = cb.s(0);                 /* sorted: buf[0] is the maximum (src/sampler.c:173-176) */
-        if (spinf) {
-            /* +inf at the top of the sorted candidates, no NaN: e is NaN there and 0
-             * elsewhere, so the sum, every probability and every comparison of the
+        if (spinf || !(R.maxv > -INFINITY)) {
+            /* +inf at the top of the sorted candidates, or every candidate -inf (1/T
+             * infinite leaves -inf below the NaN at the maximum): e = expf(s - max_v)
+             * is NaN there, so the sum, every probability and every comparison of the
              * draw are NaN and the draw falls through to buf[k-1] (src/sampler.c:233) */
             if (t == 0) p.out_ids[row] = cb.token(k - 1);
             for (int j = t; j < n_out; j += blockDim.x) {

@@ -35,7 +35,8 @@ extern "C" {
 #define DLK_STATUS_HISTORY_TOO_LONG 1u  /* a row's history exceeded max_history: its id is -1 */
 #define DLK_STATUS_SYNC_TIMEOUT 2u      /* a cross-workgroup wait gave up: the call's ids are invalid,
                                            though each stays inside [0, vocab) */
-#define DLK_STATUS_UNSUPPORTED_ROW 4u   /* a row whose s = (l - max) / T holds NaN with top_k > 4096: its id is -1 */
+#define DLK_STATUS_UNSUPPORTED_ROW 4u   /* reserved: no row kind is refused any more (rows whose
+                                           s = (l - max) / T holds NaN with top_k > 4096 are served) */
 
 /* Penalty ops, packed low nibble first into dlk_sample_params.penalty_order. */
 #define DLK_OP_REPETITION 1u  /* src/sampler.c:21-33, once per occurrence */

@@ -39,7 +39,9 @@ sampler *sampler_create(const sampler_config *cfg);
 void sampler_free(sampler *s);
 
 /* In place on the host row: once per occurrence, negative logits multiplied by
- * `penalty`, others divided; nothing unless penalty > 1 (src/sampler.c:21-33). */
+ * `penalty`, others divided; nothing unless penalty > 1 (src/sampler.c:21-33).
+ * If the device cannot be reached the row is left as it is and stderr says so
+ * (the reference's penalties cannot fail; these have no error channel either). */
 void sampler_apply_repetition_penalty(float *logits, int vocab_size, const int *seen_tokens, int num_seen,
                                       float penalty);
 
@@ -50,12 +52,18 @@ void sampler_apply_presence_penalty(float *logits, int vocab_size, const int *se
 
 /* One token from the row (src/sampler.c:136-234); advances the rng state once
  * unless temperature == 0.  The row is not modified.  Every configuration of the
- * reference is served (any non-zero temperature, any 0 < top_k < vocab_size).
- * Returns -1 only when the device call fails, or for a row whose
- * (l - max) / temperature holds NaN while top_k > 4096. */
+ * reference is served (any non-zero temperature, any 0 < top_k < vocab_size,
+ * NaN and infinite logits).  Like the reference it always returns a token in
+ * [0, vocab_size): a launch whose cross-workgroup wait gave up (another kernel
+ * holding the GPU) is run again on the one-workgroup-per-row kernel from the same
+ * rng state, and if the device cannot be reached the row is sampled greedily on
+ * the host without drawing, as the reference does when it cannot get its work
+ * buffer (src/sampler.c:145-147); that case is reported once on stderr.
+ * -1 only for a NULL sampler or row, or vocab_size <= 0. */
 int sampler_sample(sampler *s, float *logits, int vocab_size);
 
-/* First index of the maximum; 0 when logits[0] is NaN (src/sampler.c:9-19). */
+/* First index of the maximum; 0 when logits[0] is NaN (src/sampler.c:9-19).
+ * On the host if the device cannot be reached (reported once on stderr). */
 int greedy_sample(const float *logits, int vocab_size);
 
 #ifdef __cplusplus

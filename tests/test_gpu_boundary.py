@@ -52,7 +52,7 @@ def _row(rng, V, kind):
 
 BOUNDARY = [(-0.5, 0, 0.9, 0.0), (-0.5, 40, 0.95, 0.0), (-2.0, 0, 1.0, 0.05), (1e-40, 0, 0.9, 0.0),
             (1e-40, 7, 1.0, 0.0), (float("inf"), 0, 0.9, 0.0), (0.8, 5000, 0.95, 0.0), (-0.7, 5000, 0.9, 0.0),
-            (1.0, 100000, 0.9, 0.0)]
+            (1.0, 100000, 0.9, 0.0), (1e-40, 5000, 0.9, 0.0), (float("inf"), 6000, 0.9, 0.0)]
 
 
 @needs_ref
@@ -81,6 +81,53 @@ def test_dropin_boundary_vs_reference(cuda, V, cfg):
             ta = L.sampler_sample(s, fptr(a), V)
             tb = REF.sampler_sample(r, fptr(b), V)
             assert ta == tb, (V, cfg, kind, ta, tb)
+    finally:
+        L.sampler_free(s)
+        REF.sampler_free(r)
+
+
+NAN_ROWS = ["nan-inside-k", "nan-at-k-1", "nan-at-0", "nan-past-k", "pinf", "two-nans", "all-masked-one-nan"]
+
+
+@needs_ref
+@pytest.mark.parametrize("V,k", [(20000, 5000), (151936, 9000)])
+@pytest.mark.parametrize("kind", NAN_ROWS)
+def test_nan_rows_large_k_vs_reference(cuda, V, k, kind):
+    """Rows whose s = (l - max) / T holds NaN with top_k above 4096 (the
+    one-thread emulation's limit): the reference's insertion sort in closed form
+    (the window after the last NaN among the first k), or, with every NaN past
+    the first k, the ordinary selection with NaN keys last.  Token and rng
+    sequence through the drop-in against the reference build, two steps."""
+    L = _lib.lib()
+    _ref_sampler_api()
+    rng = np.random.default_rng(V + k + len(kind))
+    seed = int(rng.integers(1, 2 ** 63))
+    cfgc, rcfg = _lib.SamplerConfig(0.9, k, 0.95, 0.0, seed), O.SamplerConfig(0.9, k, 0.95, 0.0, seed)
+    s, r = L.sampler_create(C.byref(cfgc)), REF.sampler_create(C.byref(rcfg))
+    assert s and r
+    try:
+        for step in range(2):
+            _announce(f"NaN row V={V} k={k} kind={kind} step={step}")
+            row = rng.normal(0, 3, V).astype(np.float32)
+            if kind == "nan-inside-k":
+                row[rng.integers(0, k - 1, 3)] = np.nan
+            elif kind == "nan-at-k-1":
+                row[k - 1] = np.nan
+            elif kind == "nan-at-0":
+                row[0] = np.nan
+            elif kind == "nan-past-k":
+                row[rng.integers(k, V, 5)] = np.nan
+            elif kind == "pinf":
+                row[rng.integers(0, V, 2)] = np.inf
+            elif kind == "two-nans":
+                row[[rng.integers(0, k // 2), k - 2]] = np.nan
+            else:
+                row[:] = -np.inf
+                row[rng.integers(1, V)] = np.nan
+            a, b = row.copy(), row.copy()
+            ta = L.sampler_sample(s, fptr(a), V)
+            tb = REF.sampler_sample(r, fptr(b), V)
+            assert ta == tb, (V, k, kind, step, ta, tb)
     finally:
         L.sampler_free(s)
         REF.sampler_free(r)
