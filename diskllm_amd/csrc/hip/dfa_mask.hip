@@ -4,9 +4,14 @@
  * No reference counterpart: the reference validates buffer+piece from scratch
  * for every token through the accept_str callback (src/core/grammar.c:284-306);
  * for a byte-level automaton the same per-token decision is a walk of the token's
- * bytes from the current state.  The transition table (<= 64 KB) sits in LDS; one
- * thread walks one token for every row of its row group, and a wave ballot packs
- * 64 decisions into two mask words (bit t%32 of word t/32, 1 = allowed).
+ * bytes from the current state.
+ *
+ * Two kernels.  Automata of up to 64 states (dfa_walk_kernel): a wave's lanes
+ * are the rows (their start states) and the tokens are shared by the wave, so
+ * every step of every lane reads the same row of a byte-major table -- one LDS
+ * row of 68 bytes, no bank conflicts -- and the token's bytes come from LDS as
+ * broadcast reads.  Larger automata (dfa_mask_kernel): one thread per token
+ * walking it for every row of its row group.
  */
 #include "dlk_device.h"
 #include "../../../include/diskllm_amd.h"
@@ -119,6 +124,204 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
     }
 }
 
+/* ---- automata of up to 64 states ------------------------------------------
+ *
+ * LDS table tt[c * kWalkNsp + s], c = 0..255 a byte and c = 256 the end of a
+ * token, s = 0..63 a state and s = kWalkAcc (64) "accepted":
+ *   tt[c][s] = trans[s][c] for a byte (0 for s = 0 or an entry outside the table),
+ *   tt[256][s] = kWalkAcc for a live s, 0 for s = 0,
+ *   tt[c][kWalkAcc] = kWalkAcc.
+ * So a walk is one lookup per entry of the token's entry list (its bytes, then
+ * the end entry), both 0 and kWalkAcc absorb, and the token is allowed iff the
+ * walk ends at kWalkAcc.  A state is still walking iff its low 6 bits are set.
+ *
+ * A block covers a range of mask words (32 tokens each) for the RW rows of its
+ * row group (grid.y).  It stages its tokens' entry lists in LDS as u16 table
+ * offsets c * kWalkNsp, back to back, each closed by the end entry, and the
+ * list start of every token (bit 31: not walked -- empty, the EOS id, or past
+ * the vocabulary).  Lane l of a wave walks row l % RW for token slot l / RW
+ * (64 / RW slots), kWalkTpl tokens at once (independent lookups in flight); the
+ * slots' bits are OR-ed across lanes and one lane per row writes the word.
+ * Walks of one group step together until no lane of the wave is walking: a
+ * lane reads past its own end entry into the next lists or the padding of end
+ * entries after the last (as long as the block's longest list), harmlessly,
+ * since its state then absorbs.  A block whose lists exceed the staging
+ * capacity reads the bytes from global memory instead. */
+constexpr int kWalkThreads = 512;            /* one token per thread while staging */
+constexpr int kWalkAcc = 64;
+constexpr int kWalkNsp = 68;                   /* bytes per table row: 64 states, accepted, padding */
+constexpr int kWalkTabBytes = ((257 * kWalkNsp) + 15) & ~15;
+constexpr int kWalkTplMax = 8;                /* tokens walked at once per lane (at most) */
+constexpr int kWalkWpb = kWalkThreads / 32;    /* mask words per block */
+constexpr int kWalkRawPer = 16;                /* token bytes staged per thread (coalesced byte loads) */
+constexpr int kWalkRawCap = kWalkRawPer * kWalkThreads;
+constexpr int kWalkStageEntries = 10240;       /* u16 entries staged per block */
+constexpr uint32_t kWalkSkip = 0x80000000u;
+constexpr size_t kWalkLds = kWalkTabBytes + kWalkWpb * 32 * 4 + kWalkRawCap + kWalkStageEntries * 2;
+
+/* byte k of x if it is a state of the automaton, else 0 */
+__device__ __forceinline__ uint32_t live_byte(uint32_t x, int k, uint32_t n_states) {
+    const uint32_t v = (x >> (8 * k)) & 255u;
+    return v < n_states ? v : 0u;
+}
+
+template <int RW>
+__global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *__restrict__ off,
+                                                                const uint8_t *__restrict__ bytes, int V,
+                                                                const uint8_t *__restrict__ trans, int n_states,
+                                                                const int32_t *__restrict__ states, int n_rows,
+                                                                int eos_id, uint64_t accept,
+                                                                uint32_t *__restrict__ out, int64_t ld) {
+    constexpr int P = 64 / RW;                 /* token slots per wave */
+    constexpr int kWalkTpl = 32 / P < kWalkTplMax ? 32 / P : kWalkTplMax;   /* tokens per lane */
+    constexpr int TPI = P * kWalkTpl;          /* tokens per wave iteration (divides 32) */
+    static_assert(32 % TPI == 0, "an iteration's tokens lie in one mask word");
+    extern __shared__ __align__(16) uint8_t sm[];
+    __shared__ uint32_t s_maxlen;
+    uint8_t *tt = sm;
+    uint32_t *tpos = (uint32_t *)(sm + kWalkTabBytes);                     /* [kWalkWpb * 32] */
+    uint8_t *raw = sm + kWalkTabBytes + kWalkWpb * 32 * 4;                 /* [kWalkRawCap] */
+    uint16_t *ent = (uint16_t *)(raw + kWalkRawCap);                       /* [kWalkStageEntries] */
+    const int t = threadIdx.x;
+    const int W = (V + 31) >> 5;
+    const int w0 = blockIdx.x * kWalkWpb, w1 = min(W, w0 + kWalkWpb);
+    const int t0 = w0 * 32, t1 = min(V, w1 * 32);
+    const uint32_t ns = (uint32_t)n_states;
+    /* ---- every global load first: the table as 4x4 byte squares (states 4a..,
+     *      bytes 4q..; two squares per thread, coalesced over q), the token's
+     *      offsets, and the block's token bytes (coalesced bytes) ------------- */
+    uint32_t sq[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int i = t + h * kWalkThreads, a = i >> 6, q = i & 63;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int st = 4 * a + k;
+            sq[h][k] = (st > 0 && st < n_states) ? *(const uint32_t *)(trans + st * 256 + 4 * q) : 0u;
+        }
+    }
+    const int tk = t0 + t;                     /* this thread's token (kWalkWpb * 32 == kWalkThreads) */
+    uint32_t b0 = 0, len = 0;
+    if (tk < t1) {
+        b0 = off[tk];
+        len = off[tk + 1] - b0;
+    }
+    const uint32_t B = off[t0];
+    const uint32_t n_raw = off[t1] - B;
+    uint32_t rb[kWalkRawPer];
+#pragma unroll
+    for (int m = 0; m < kWalkRawPer; m++) {
+        const uint32_t i = (uint32_t)t + (uint32_t)m * kWalkThreads;
+        rb[m] = i < n_raw ? bytes[B + i] : 0u;
+    }
+    /* ---- LDS: the table byte-major, the bytes, the longest entry list -------- */
+    if (t == 0) s_maxlen = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int i = t + h * kWalkThreads, a = i >> 6, q = i & 63;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t x = live_byte(sq[h][0], m, ns) | (live_byte(sq[h][1], m, ns) << 8) |
+                               (live_byte(sq[h][2], m, ns) << 16) | (live_byte(sq[h][3], m, ns) << 24);
+            *(uint32_t *)(tt + (4 * q + m) * kWalkNsp + 4 * a) = x;
+        }
+    }
+    if (t < 257) *(uint32_t *)(tt + t * kWalkNsp + kWalkAcc) = (uint32_t)kWalkAcc;   /* accepted absorbs */
+    if (t < 16) {                                                                    /* the end row */
+        uint32_t x = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int st = 4 * t + k;
+            x |= (st > 0 && st < n_states ? (uint32_t)kWalkAcc : 0u) << (8 * k);
+        }
+        *(uint32_t *)(tt + 256 * kWalkNsp + 4 * t) = x;
+    }
+#pragma unroll
+    for (int m = 0; m < kWalkRawPer; m++) {
+        const uint32_t i = (uint32_t)t + (uint32_t)m * kWalkThreads;
+        if (i < n_raw && i < (uint32_t)kWalkRawCap) raw[i] = (uint8_t)rb[m];
+    }
+    __syncthreads();
+    if (tk < t1) atomicMax(&s_maxlen, len + 1);
+    __syncthreads();
+    /* ---- each token's entry list: its bytes as table rows, then the end row --- */
+    const uint32_t n_ent = n_raw + (uint32_t)(t1 - t0);
+    const uint32_t pad = s_maxlen;       /* a walk reads at most this far past a list start */
+    const bool staged = n_raw <= (uint32_t)kWalkRawCap && (uint64_t)n_ent + pad <= (uint64_t)kWalkStageEntries;
+    const uint32_t p0 = b0 - B + (uint32_t)t;
+    if (staged) {
+        for (uint32_t j = 0; j < len; j++) ent[p0 + j] = (uint16_t)(raw[b0 - B + j] * kWalkNsp);
+        if (tk < t1) ent[p0 + len] = (uint16_t)(256 * kWalkNsp);
+        for (uint32_t i = (uint32_t)t; i < pad; i += kWalkThreads) ent[n_ent + i] = (uint16_t)(256 * kWalkNsp);
+    }
+    tpos[t] = (tk >= t1 || len == 0 || tk == eos_id) ? kWalkSkip : p0;
+    __syncthreads();
+    /* ---- the walks -------------------------------------------------------------- */
+    const int lane = lane_id(), wv = t >> 6, slot = lane / RW;
+    const int r = blockIdx.y * RW + lane % RW;
+    const int s_row = r < n_rows ? states[r] : 0;
+    const uint32_t s_init = (s_row > 0 && s_row < n_states) ? (uint32_t)s_row : 0u;
+    const bool eos_ok = s_row > 0 && s_row < 64 && ((accept >> s_row) & 1ull);
+    for (int w = w0 + wv; w < w1; w += kWalkThreads / 64) {
+        uint32_t bits = 0;
+#pragma unroll 1
+        for (int it = 0; it < 32; it += TPI) {
+            const int tb = w * 32 + it + slot * kWalkTpl;          /* this lane's first token */
+            uint32_t st[kWalkTpl], pos[kWalkTpl];
+#pragma unroll
+            for (int i = 0; i < kWalkTpl; i++) {
+                const uint32_t pp = tpos[tb + i - t0];
+                pos[i] = pp & ~kWalkSkip;
+                st[i] = (pp & kWalkSkip) ? 0u : s_init;
+            }
+            if (staged) {
+                /* two steps per check: a walk that has absorbed stays where it is */
+                while (true) {
+                    uint32_t act = 0;
+#pragma unroll
+                    for (int i = 0; i < kWalkTpl; i++) act |= st[i];
+                    if (ballot((act & 63u) != 0u) == 0) break;
+#pragma unroll
+                    for (int i = 0; i < kWalkTpl; i++) {
+                        const uint32_t e0 = ent[pos[i]], e1 = ent[pos[i] + 1];
+                        st[i] = tt[e1 + tt[e0 + st[i]]];
+                        pos[i] += 2;
+                    }
+                }
+            } else {
+                uint32_t tb0[kWalkTpl], tlen[kWalkTpl];
+#pragma unroll
+                for (int i = 0; i < kWalkTpl; i++) {
+                    const int tq = tb + i;
+                    tb0[i] = tq < t1 ? off[tq] : 0u;
+                    tlen[i] = tq < t1 ? off[tq + 1] - tb0[i] : 0u;
+                }
+                for (uint32_t j = 0;; j++) {
+                    uint32_t act = 0;
+#pragma unroll
+                    for (int i = 0; i < kWalkTpl; i++) act |= st[i];
+                    if (ballot((act & 63u) != 0u) == 0) break;
+#pragma unroll
+                    for (int i = 0; i < kWalkTpl; i++) {
+                        const uint32_t c = j < tlen[i] ? (uint32_t)bytes[tb0[i] + j] : (j == tlen[i] ? 256u : 0u);
+                        const uint32_t nx = tt[c * kWalkNsp + st[i]];
+                        st[i] = j <= tlen[i] ? nx : st[i];
+                    }
+                }
+            }
+            /* (the EOS id is not walked: its state is 0 here, its bit set below) */
+            uint32_t nib = 0;
+#pragma unroll
+            for (int i = 0; i < kWalkTpl; i++) nib |= (st[i] == (uint32_t)kWalkAcc ? 1u : 0u) << i;
+            bits |= nib << (it + slot * kWalkTpl);
+        }
+#pragma unroll
+        for (int m = RW; m < 64; m <<= 1) bits |= (uint32_t)shfl_xor((int)bits, m);
+        if (eos_id >= w * 32 && eos_id < w * 32 + 32 && eos_id < V && eos_ok) bits |= 1u << (eos_id & 31);
+        if (slot == 0 && r < n_rows) out[(int64_t)r * ld + w] = bits;
+    }
+}
+
 }  // namespace dlk
 
 extern "C" int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab, const uint8_t *trans,
@@ -128,6 +331,48 @@ extern "C" int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab
     if (n_states <= 0 || n_states > 256) return DLK_ERR_UNSUPPORTED;
     if (mask_ld < (vocab + 31) / 32) return DLK_ERR_INVALID;
     if (((uintptr_t)trans & 3) != 0) return DLK_ERR_INVALID;
+    if (n_states <= 64) {
+        /* the row-per-lane walk (dfa_walk_kernel) */
+        const int W = (vocab + 31) / 32;
+        const int RW = n_rows <= 8 ? 8 : n_rows <= 16 ? 16 : n_rows <= 32 ? 32 : 64;
+        const dim3 grid((unsigned)((W + dlk::kWalkWpb - 1) / dlk::kWalkWpb), (unsigned)((n_rows + RW - 1) / RW));
+        if (grid.y > 65535) return DLK_ERR_UNSUPPORTED;
+        const size_t lds = dlk::kWalkLds;
+        auto launch = [&](const void *fn) -> int {
+            static int attr[4] = {0, 0, 0, 0};
+            const int ai = RW == 8 ? 0 : RW == 16 ? 1 : RW == 32 ? 2 : 3;
+            if (!attr[ai]) {
+                if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+                    return DLK_ERR_HIP;
+                attr[ai] = 1;
+            }
+            return DLK_OK;
+        };
+        int rc;
+        switch (RW) {
+        case 8:
+            if ((rc = launch((const void *)dlk::dfa_walk_kernel<8>)) != DLK_OK) return rc;
+            hipLaunchKernelGGL(dlk::dfa_walk_kernel<8>, grid, dim3(dlk::kWalkThreads), lds, stream, off, bytes, vocab,
+                               trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+            break;
+        case 16:
+            if ((rc = launch((const void *)dlk::dfa_walk_kernel<16>)) != DLK_OK) return rc;
+            hipLaunchKernelGGL(dlk::dfa_walk_kernel<16>, grid, dim3(dlk::kWalkThreads), lds, stream, off, bytes,
+                               vocab, trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+            break;
+        case 32:
+            if ((rc = launch((const void *)dlk::dfa_walk_kernel<32>)) != DLK_OK) return rc;
+            hipLaunchKernelGGL(dlk::dfa_walk_kernel<32>, grid, dim3(dlk::kWalkThreads), lds, stream, off, bytes,
+                               vocab, trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+            break;
+        default:
+            if ((rc = launch((const void *)dlk::dfa_walk_kernel<64>)) != DLK_OK) return rc;
+            hipLaunchKernelGGL(dlk::dfa_walk_kernel<64>, grid, dim3(dlk::kWalkThreads), lds, stream, off, bytes,
+                               vocab, trans, n_states, states, n_rows, eos_id, accept_mask, out_mask, mask_ld);
+            break;
+        }
+        return hipGetLastError() == hipSuccess ? DLK_OK : DLK_ERR_HIP;
+    }
     const int R = n_rows <= 16 ? 8 : 16;
     const int n_groups = (n_rows + R - 1) / R, tok_blocks = (vocab + 255) / 256;
     int gpb = (int)std::min<int64_t>(n_groups, std::max<int64_t>(1, (int64_t)tok_blocks * n_groups / 1024));
