@@ -505,6 +505,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-runs", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--temperature", type=float, default=1.0,
+                    help="C2 at another temperature (the configuration's is 1.0; lower ones sharpen the rows)")
     ap.add_argument("--batches", type=int, default=12,
                     help="C2: distinct batches resident in HBM, one per step in turn (12 x 38.96 MB = 468 MB)")
     ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "C5CAP", "CAP", "DROPIN"],
@@ -545,6 +547,8 @@ def main() -> int:
     # logits from HBM and meets its own rows' sums, as a decode loop does
     NB = max(1, args.batches)
     ws = [workloads.c2(seed=2 + 7919 * b) for b in range(NB)]
+    for wb in ws:
+        wb.temperature = args.temperature
     dbs = [api.to_device(w, device=dev) for w in ws]
     w, db = ws[0], dbs[0]
     params = api.params_of(w)
@@ -622,7 +626,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "C2: batch-64 full-vocab nucleus sampling, fp32 logits [64,151936], rep 1.15 / "
-                               "freq 0.3 / pres 0.5 over 256-id Zipf history, T 1.0, top-p 0.9, no top-k",
+                               f"freq 0.3 / pres 0.5 over 256-id Zipf history, T {args.temperature:g}, top-p 0.9, "
+                               "no top-k",
                    "rows": ROWS, "vocab": VOCAB, "history": HIST, "parallelism": "none (1 GPU)",
                    "batches": NB, "resident_bytes": NB * bytes_launch,
                    "step": f"one dlk_sample call on batch (step mod {NB}): {NB} distinct C2 batches "

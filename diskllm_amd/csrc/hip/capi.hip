@@ -301,17 +301,21 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     memset(&f, 0, sizeof(f));
     f.G = G;
     f.S = S;
-    f.stage_cap = 64;
     f.force_exact = force_exact;
     f.no_wait = no_wait;
-    /* carve order of full_kernel: sbits, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, seg,
-     * tab, tbase, rres, rbase, pc, misc, md */
-    const size_t lds = fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
-                       2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
-                       r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)f.stage_cap * 64 * 4) +
-                       r16((size_t)nch * 8) + r16((size_t)nch * 16) + r16((size_t)kMaxTabs * 64 * 8) +
-                       r16((size_t)kMaxTabs * 4) + r16((size_t)(kFullThreads / 64) * 64 * 8) +
-                       r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
+    /* carve order of full_kernel: sbits, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, elc, seg,
+     * tab, tbase, rres, rbase, pc, misc, md; chunks staged per workgroup: 96 where LDS allows (sharp rows
+     * stage many chunks: every one with a tie and those around r's crossing), else 64 */
+    auto lds_for = [&](int stage_cap) {
+        return fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
+               2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
+               r16((size_t)(nch + 1) * 8) + r16((size_t)nch * 4) + 2 * r16((size_t)stage_cap * 64 * 4) +
+               r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 16) + r16((size_t)kMaxTabs * 64 * 8) +
+               r16((size_t)kMaxTabs * 4) + r16((size_t)(kFullThreads / 64) * 64 * 8) +
+               r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
+    };
+    f.stage_cap = lds_for(96) <= kMaxLds ? 96 : 64;
+    const size_t lds = lds_for(f.stage_cap);
     if (lds > kMaxLds) return 1;
     /* resident workgroups of this instance: queried once per (device, ept, LDS) */
     struct CapEntry { int dev, ept; size_t lds; int softcap, cap; };

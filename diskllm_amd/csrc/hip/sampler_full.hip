@@ -180,6 +180,82 @@ DLK_DEV uint64_t block_incl_prefix_u64(uint64_t v, uint64_t *red) {
     return base + inc;
 }
 
+/* The draw's per-slice data in LDS (see full_kernel): segments, run
+ * increments, staged chunks and candidate tables. */
+struct DrawView {
+    const int4 *seg;
+    const uint64_t *rtot;
+    const int *smap;
+    const uint32_t *spx;
+    const int2 *tab;
+    const uint32_t *tbase;
+    int ntab, nch_loc, s0;
+    float thr_f;
+};
+
+/* One segment s of the draw for the lane's running value (bits cb): a run adds
+ * its increments (exact while the value stays in the run's binade), an
+ * element-level chunk is a table lookup.  tok becomes the token on a crossing,
+ * or -2 when unresolved (a value outside what the prediction covers).  (Code
+ * that let a lane sum a chunk outside its table itself, even out of this path
+ * and never run, made every launch 17 us slower, so a value outside a table is
+ * unresolved here and the tables are recentred on the refined starts.) */
+__device__ __forceinline__ void draw_step(const DrawView &dv, int s, uint32_t &cb, int &tok) {
+    const int4 sg = dv.seg[s];
+    const int sx = sg.x, sy = sg.y, sz = sg.z, sw = sg.w;
+    const float thr_f = dv.thr_f;
+    if (sx == kZeroBinade) return;
+    if (sx != kInvalidBinade) {
+        /* run [sy, sw) on the grid of binade sx: exact integer steps
+         * on the value's bits while it stays in the binade */
+        const uint32_t R = (uint32_t)sz;
+        const bool inb = (cb >> 23) == (uint32_t)(sx + 127) && (cb & 0x7fffffu) + R < 0x800000u;
+        if (!inb) {
+            tok = -2;
+        } else if (u2f(cb + R) >= thr_f) {
+            /* the crossing is in this run: its chunk by bisection on
+             * the increments to the run's end, then its element */
+            const uint64_t R0 = dv.rtot[sy];
+            int lo = sy, hi = sw - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                const uint64_t after = mid + 1 < sw ? dv.rtot[mid + 1] : 0ull;
+                if (u2f(cb + (uint32_t)(R0 - after)) >= thr_f) hi = mid;
+                else lo = mid + 1;
+            }
+            const int sl = dv.smap[lo];
+            tok = -2;
+            if (sl >= 0) {
+                /* the first element whose running value (the chunk's
+                 * start plus its increment prefix, on one grid) reaches
+                 * thr_f: a bisection on the prefixes */
+                const uint32_t need = f2u(thr_f) - (cb + (uint32_t)(R0 - dv.rtot[lo]));
+                const uint32_t *px = dv.spx + sl * 64;
+                int ea = 0, eb = 63;
+                while (ea < eb) {
+                    const int em = (ea + eb) >> 1;
+                    if (px[em] >= need) eb = em;
+                    else ea = em + 1;
+                }
+                tok = dv.s0 + 64 * lo + ea;
+            }
+        } else {
+            cb += R;
+        }
+    } else {
+        /* element-level chunk sy: its table sz */
+        const uint32_t bse = sz < dv.ntab ? dv.tbase[sz] : 0xffffffffu;
+        const uint32_t d = cb - bse;
+        if (bse == 0xffffffffu || d >= 64u) {
+            tok = -2;
+        } else {
+            const int2 te = dv.tab[sz * 64 + (int)d];
+            if (te.y >= 0) tok = dv.s0 + 64 * sy + te.y;
+            else cb = (uint32_t)te.x;
+        }
+    }
+}
+
 /* NOWAIT (a test instance): every wait gives up at its first poll that finds a
  * word not yet written, which sets DLK_STATUS_SYNC_TIMEOUT. */
 template <int EPT, bool CAP, bool NOWAIT = false>
@@ -213,6 +289,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     float *svals = (float *)carve(q, (size_t)f.stage_cap * 64 * 4);
     uint32_t *spx = (uint32_t *)carve(q, (size_t)f.stage_cap * 64 * 4);   /* staged run chunks: increment prefixes */
     int2 *elist = (int2 *)carve(q, (size_t)nch * 8);             /* element-level chunks {chunk, slot} */
+    int *elc = (int *)carve(q, (size_t)nch * 4);                 /* element-level chunks before chunk c */
     int4 *seg = (int4 *)carve(q, (size_t)nch * 16);              /* the draw's segments */
     int2 *tab = (int2 *)carve(q, (size_t)kMaxTabs * 64 * 8);     /* candidate tables {end bits, crossing} */
     uint32_t *tbase = (uint32_t *)carve(q, (size_t)kMaxTabs * 4);  /* each table's first candidate */
@@ -757,6 +834,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const uint64_t ainc = all & ((1ull << 40) - 1);
         const uint32_t run = (uint32_t)((all >> 40) & 0xfffu) - (end ? 1u : 0u);
         if (isel) elpos = (int)(all >> 52) - 1;
+        if (in) elc[c] = (int)(all >> 52) - (isel ? 1 : 0);
         if (t == T - 1) {
             misc[17] = (int)(all >> 52);
             misc[21] = (int)((all >> 40) & 0xfffu);
@@ -778,8 +856,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     /* each chunk's predicted contribution to the exact float running sum: its
      * increments on its binade's grid (exact while the prediction holds), or
      * the real sum of an element-level chunk (off by that chunk's rounding, a
-     * few of its ulps); the chunks staged in LDS: the element-level ones, the
-     * ones that may hold r's crossing, and x's */
+     * few of its ulps); the chunks staged in LDS here: the element-level ones
+     * and x's (those that may hold r's crossing follow barrier D) */
     double *fpre = ce;                             /* ce is free again */
     const float thr_f = u2f(f2u(r) + 1u);          /* r < cumul  <=>  cumul >= thr_f */
     const double vthr = (double)thr_f;
@@ -787,9 +865,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int c = t;
         const int bh = cbh[c];
         fpre[c] = bh != kInvalidBinade ? ldexp((double)ca[c], bh - 23) : Pc[c + 1] - Pc[c];
-        const double a = Pc[c], b = Pc[c + 1], m2 = 0x1p-9;
-        const bool want = bh == kInvalidBinade || (a * (1.0 - m2) <= vthr && vthr <= b * (1.0 + m2)) ||
-                          (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
+        const bool want = bh == kInvalidBinade || (x >= s0 + 64 * c && x < s0 + 64 * c + 64);
         int sl = -1;
         if (want && s0 + 64 * c <= x) {
             sl = atomicAdd(&misc[10], 1);
@@ -802,26 +878,32 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     block_excl_scan(fpre, nch, L.red);             /* fpre[c]: before chunk c; fpre[nch]: the slice */
     if (t == 0) at_st64(&mypub[kPubF], d2u(fpre[nch]) | kReady);
     /* a staged chunk's values, and for a chunk of a run the inclusive prefix of
-     * its increments on the run's grid (a chunk is one 16-lane row) */
+     * its increments on the run's grid (a chunk is one 16-lane row); slot_of
+     * gives the chunk's slot, or -1 for a chunk not staged by this pass */
+    auto stage = [&](const int *slot_of) {
 #pragma unroll
-    for (int j4 = 0; j4 < EPT / 4; j4++) {
-        const int u = t + j4 * T;
-        const int c = u >> 4;
-        const int sl = smap[c];
-        if (ballot(sl >= 0) != 0) {
-            const int bh = cbh[c];
-            const bool run = bh != kInvalidBinade && bh != kZeroBinade;
-            uint32_t n[4];
+        for (int j4 = 0; j4 < EPT / 4; j4++) {
+            const int u = t + j4 * T;
+            const int c = u >> 4;
+            const int sl = slot_of[c];
+            if (ballot(sl >= 0) != 0) {
+                const int bh = cbh[c];
+                const bool run = bh != kInvalidBinade && bh != kZeroBinade;
+                uint32_t n[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) n[k] = run ? (uint32_t)rintf(ldexpf(v[4 * j4 + k], 23 - bh)) : 0u;
-            const uint32_t s4 = ((n[0] + n[1]) + n[2]) + n[3];
-            const uint32_t ex = row_scan_u32(s4) - s4;
-            if (sl >= 0) {
-                *(float4 *)&svals[sl * 64 + (u & 15) * 4] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
-                *(uint4 *)&spx[sl * 64 + (u & 15) * 4] = make_uint4(ex + n[0], ex + n[0] + n[1], ex + n[0] + n[1] + n[2], ex + s4);
+                for (int k = 0; k < 4; k++) n[k] = run ? (uint32_t)rintf(ldexpf(v[4 * j4 + k], 23 - bh)) : 0u;
+                const uint32_t s4 = ((n[0] + n[1]) + n[2]) + n[3];
+                const uint32_t ex = row_scan_u32(s4) - s4;
+                if (sl >= 0) {
+                    *(float4 *)&svals[sl * 64 + (u & 15) * 4] =
+                        make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+                    *(uint4 *)&spx[sl * 64 + (u & 15) * 4] =
+                        make_uint4(ex + n[0], ex + n[0] + n[1], ex + n[0] + n[1] + n[2], ex + s4);
+                }
             }
         }
-    }
+    };
+    stage(smap);
 
     /* ---- D: the slices' predicted contributions -> this slice's predicted
      *      exact start value (exact for slice 0: the sum starts at 0) ------- */
@@ -832,38 +914,86 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double Phat = 0.0;
     for (int h = 0; h < g; h++) Phat += u2d(pc[h * kPubWords + kPubF]);
 
+    /* ---- the chunks that may hold r's crossing, from the float prediction
+     *      (this slice's predicted start plus its contributions, off by a few
+     *      tens of its ulps at most on sharp rows): a chunk that adds something
+     *      and whose predicted running values come within 128 ulps of thr_f.
+     *      (A window on the double prefix, whose drift from the float sum is
+     *      some 10^-4 relative, took hundreds of nearly empty chunks of sharp
+     *      rows and overflowed the staging.)  rend (free after the segments)
+     *      holds the slots of this pass. ---------------------------------- */
+    {
+        const uint32_t ex_thr = (f2u(thr_f) >> 23) & 255u;
+        const double mg = 128.0 * ldexp(1.0, (int)(ex_thr > 0u ? ex_thr : 1u) - 150);
+        /* (a slice whose predicted span misses thr_f by more than the margin
+         * stages nothing here: every workgroup evaluates the same test) */
+        const bool span = Phat + fpre[0] - mg <= vthr && vthr <= Phat + fpre[nch] + mg && s0 <= x;
+        if (span && t < nch) {
+            const int c = t;
+            int sl = -1;
+            if (smap[c] < 0 && s0 + 64 * c <= x && cbh[c] != kZeroBinade) {
+                const double a = Phat + fpre[c], b = Phat + fpre[c + 1];
+                if (a - mg <= vthr && vthr <= b + mg) {
+                    sl = atomicAdd(&misc[10], 1);
+                    if (sl >= f.stage_cap) sl = -1;
+                    else smap[c] = sl;
+                }
+            }
+            rend[c] = sl;
+        }
+        if (span) {
+            __syncthreads();
+            stage(rend);
+        }
+    }
+
     /* ---- candidate tables: each element-level chunk summed in order from the
      *      64 consecutive floats around its predicted start, one wave per chunk
      *      (src/sampler.c:226-232); lane k keeps the end value and the first
      *      position whose running value reaches thr_f ------------------------ */
     const int ntab = min(misc[17], kMaxTabs);
+    /* table ti for the 64 starts from `base`: lane k's end value and crossing
+     * (returned: the lane's end value) */
+    auto build_table = [&](int ti, const int2 e, uint32_t base) -> float {
+        float c = u2f(base + (uint32_t)lane);
+        int below = 0;
+        const float4 *q4 = (const float4 *)(svals + e.y * 64);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const float4 qv = q4[k];
+            c = c + qv.x;
+            below += c < thr_f ? 1 : 0;
+            c = c + qv.y;
+            below += c < thr_f ? 1 : 0;
+            c = c + qv.z;
+            below += c < thr_f ? 1 : 0;
+            c = c + qv.w;
+            below += c < thr_f ? 1 : 0;
+        }
+        tab[ti * 64 + lane] = make_int2((int)f2u(c), below < 64 ? below : -1);
+        return c;
+    };
+    /* each table's correction to its chunk's predicted contribution: lane 32
+     * starts at the chunk's predicted value, so its end value less that start
+     * is the chunk's float contribution (the same for any start on that grid,
+     * ties and binade changes aside), where the prediction took the chunk's
+     * real sum, off by its additions' roundings (L.red is free from here to
+     * the end of the ranges) */
+    double *tdelta = L.red;
     for (int ti = wave_id(); ti < ntab; ti += T / 64) {
         const int2 e = elist[ti];
         uint32_t base = 0xffffffffu;
+        double dl = 0.0;
         if (e.y >= 0) {
             const uint32_t pb = f2u((float)(Phat + fpre[e.x]));
             base = pb >= 32u ? pb - 32u : 0u;
-            float c = u2f(base + (uint32_t)lane);
-            int below = 0;
-            const float4 *q4 = (const float4 *)(svals + e.y * 64);
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float4 qv = q4[k];
-                c = c + qv.x;
-                below += c < thr_f ? 1 : 0;
-                c = c + qv.y;
-                below += c < thr_f ? 1 : 0;
-                c = c + qv.z;
-                below += c < thr_f ? 1 : 0;
-                c = c + qv.w;
-                below += c < thr_f ? 1 : 0;
-            }
-            tab[ti * 64 + lane] = make_int2((int)f2u(c), below < 64 ? below : -1);
+            const float cend = build_table(ti, e, base);
+            dl = (double)cend - (double)u2f(base + 32u) - (fpre[e.x + 1] - fpre[e.x]);
         }
         if (lane == 0) tbase[ti] = base;
+        if (lane == 32) tdelta[ti] = dl;
     }
     __syncthreads();
-
     /* ---- the slice's draw for 64 candidate start values (slice 0: its exact
      *      start 0 in every lane).  The segments are split into one contiguous
      *      range per wave; wave w runs its range for the 64 consecutive floats
@@ -883,7 +1013,47 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int w = wave_id();
         const int sa = w * per, sb = min(nseg, sa + per);
         const int c0 = seg[sa].y;
-        const double pstart = Phat + fpre[c0];
+        /* refined start: the corrections of the tables before the range (they
+         * add up over a slice's element-level chunks; without them a range's
+         * start fell outside its 64 candidates on sharper rows, T 0.7-0.8) */
+        const double dlt = lane < ntab ? tdelta[lane] : 0.0;
+        const double dex = wave_incl_scan_d(dlt) - dlt;
+        const double pstart = Phat + fpre[c0] + u2d(readlane64(d2u(dex), min(elc[c0], ntab)));
+        /* this wave alone reads the tables of its range: one whose refined start
+         * (the corrections of the tables before it) lies more than 24 candidates
+         * from its window's centre is built again around it, here, with no
+         * barrier (the corrections do not depend on where the windows lie).
+         * One lane per segment of the range; a range holds at most 64. */
+        {
+            int ti = -1;
+            uint32_t nb = 0;
+            if (sa + lane < sb) {
+                const int4 sg = seg[sa + lane];
+                if (sg.x == kInvalidBinade && sg.y < nch_loc && sg.z < ntab) ti = sg.z;
+            }
+            const double dti = u2d(((uint64_t)(uint32_t)__shfl((int)(uint32_t)(d2u(dex) >> 32), max(ti, 0), 64) << 32) |
+                                   (uint32_t)__shfl((int)(uint32_t)d2u(dex), max(ti, 0), 64));
+            bool re = false;
+            if (ti >= 0) {
+                const int2 e = elist[ti];
+                const uint32_t ob = tbase[ti];
+                if (e.y >= 0 && ob != 0xffffffffu) {
+                    const uint32_t pb = f2u((float)(Phat + fpre[e.x] + dti));
+                    nb = pb >= 32u ? pb - 32u : 0u;
+                    const int dd = (int)(nb - ob);
+                    re = dd < -24 || dd > 24;
+                }
+            }
+            uint64_t todo = ballot(re);
+            while (DLK_COLD(todo != 0)) {
+                const int l = first_lane(todo);
+                todo &= todo - 1;
+                const int tj = __builtin_amdgcn_readlane(ti, l);
+                const uint32_t nbj = (uint32_t)__builtin_amdgcn_readlane((int)nb, l);
+                build_table(tj, elist[tj], nbj);
+                if (lane == 0) tbase[tj] = nbj;
+            }
+        }
         uint32_t rb = 0, cb = 0;
         if (g > 0 || w > 0) {
             const uint32_t pb = f2u((float)pstart);
@@ -896,60 +1066,12 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         } else if (pstart > vthr * (1.0 + 0x1p-9)) {
             tok = -3;                              /* r's crossing lies before this range */
         } else {
+            const DrawView dv{seg, rtot, smap, spx, tab, tbase, ntab, nch_loc, s0, thr_f};
             for (int s = sa; s < sb; s++) {
-                const int4 sg = seg[s];
-                const int sx = sg.x, sy = sg.y, sz = sg.z, sw = sg.w;
+                const int sy = seg[s].y;
                 if (sy >= nch_loc || ballot(tok == -1) == 0) break;
-                if (tok != -1 || sx == kZeroBinade) continue;
-                if (sx != kInvalidBinade) {
-                    /* run [sy, sw) on the grid of binade sx: exact integer steps
-                     * on the value's bits while it stays in the binade */
-                    const uint32_t R = (uint32_t)sz;
-                    const bool inb = (cb >> 23) == (uint32_t)(sx + 127) && (cb & 0x7fffffu) + R < 0x800000u;
-                    if (!inb) {
-                        tok = -2;
-                    } else if (u2f(cb + R) >= thr_f) {
-                        /* the crossing is in this run: its chunk by bisection on
-                         * the increments to the run's end, then its element */
-                        const uint64_t R0 = rtot[sy];
-                        int lo = sy, hi = sw - 1;
-                        while (lo < hi) {
-                            const int mid = (lo + hi) >> 1;
-                            const uint64_t after = mid + 1 < sw ? rtot[mid + 1] : 0ull;
-                            if (u2f(cb + (uint32_t)(R0 - after)) >= thr_f) hi = mid;
-                            else lo = mid + 1;
-                        }
-                        const int sl = smap[lo];
-                        tok = -2;
-                        if (sl >= 0) {
-                            /* the first element whose running value (the chunk's
-                             * start plus its increment prefix, on one grid) reaches
-                             * thr_f: a bisection on the prefixes */
-                            const uint32_t need = f2u(thr_f) - (cb + (uint32_t)(R0 - rtot[lo]));
-                            const uint32_t *px = spx + sl * 64;
-                            int ea = 0, eb = 63;
-                            while (ea < eb) {
-                                const int em = (ea + eb) >> 1;
-                                if (px[em] >= need) eb = em;
-                                else ea = em + 1;
-                            }
-                            tok = s0 + 64 * lo + ea;
-                        }
-                    } else {
-                        cb += R;
-                    }
-                } else {
-                    /* element-level chunk sy: its table sz */
-                    const uint32_t bse = sz < ntab ? tbase[sz] : 0xffffffffu;
-                    const uint32_t d = cb - bse;
-                    if (bse == 0xffffffffu || d >= 64u) {
-                        tok = -2;
-                    } else {
-                        const int2 te = tab[sz * 64 + (int)d];
-                        if (te.y >= 0) tok = s0 + 64 * sy + te.y;
-                        else cb = (uint32_t)te.x;
-                    }
-                }
+                if (tok != -1) continue;
+                draw_step(dv, s, cb, tok);
             }
         }
         rres[w * 64 + lane] = make_int2((int)cb, tok);
