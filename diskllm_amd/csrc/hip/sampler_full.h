@@ -18,7 +18,9 @@ constexpr uint32_t kFullSpinLimit = 1u << 22;   /* polls before a cross-workgrou
 /* per-row sync words (all zero between launches) */
 enum : int {
     kSyncExit = 3,     /* workgroups finished */
-    kSyncLanes = 5     /* workgroups that published their candidate chains */
+    kSyncLanes = 5,    /* workgroups that published their candidate chains */
+    kSyncSplitE = 6,   /* workgroups that stored their slice of the split softmax sum */
+    kSyncSplitP = 7    /* workgroups that stored their slice of the split top-p cumulation */
 };
 
 /* published words per workgroup */
@@ -31,8 +33,11 @@ enum : int {
     kPubN2 = 5,        /* min-p: surviving entries in the slice */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
     kPubF = 9,         /* double: the slice's predicted contribution to the draw's float sum */
-    kPubX = 10         /* from the slice holding the top-p crossing: x (bits 0-30, 0x7fffffff: not
+    kPubX = 10,        /* from the slice holding the top-p crossing: x (bits 0-30, 0x7fffffff: not
                           certified) and the float bits of inv3 (bits 31-62) */
+    kPubSplitE = 11,   /* workgroup 0: the split softmax sum (double bits; NaN: a wait gave up) */
+    kPubSplitP = 13    /* workgroup 0: the split top-p cumulation's value (double bits) and, in
+                          the next word, its threshold position (-1: none) */
 };
 
 constexpr int kMaxTabs = 48;         /* element-level chunks with a candidate table per workgroup */
@@ -49,9 +54,11 @@ struct FullParams {
     uint64_t *lanes;   /* [rows][G][kLaneWords]: per candidate start of the slice, its end value
                           (low word) and crossing token (high word: -1 none, -2 unresolved);
                           word 64: float bits of candidate 0 */
-    unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback */
-    size_t fb_bytes;
-    int force_exact;   /* test hook: send every row through the exact fallback */
+    unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback and the split
+                          sums, then (at fb_q_off) the row's values for the split sums */
+    size_t fb_bytes, fb_q_off;
+    int force_exact;   /* test hooks: 1 sends every row through the exact fallback; 2 runs the
+                          split sums on every row (as if neither bound had decided) */
     int no_wait;       /* test hook: launch the instance whose waits give up at their first poll
                           that finds a word not yet written (DLK_STATUS_SYNC_TIMEOUT) */
 };

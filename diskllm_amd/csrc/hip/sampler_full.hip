@@ -256,6 +256,117 @@ __device__ __forceinline__ void draw_step(const DrawView &dv, int s, uint32_t &c
     }
 }
 
+/* Values of the row for the element-level steps of the split sum's walk. */
+struct QRow {
+    const float *q;
+    DLK_DEV float operator()(int i) const { return q[i]; }
+};
+
+/* A double running sum over the whole row (the softmax sum, src/sampler.c:
+ * 177-181, or the top-p cumulation, :207-215) that the certified bound could
+ * not decide, run by all G workgroups of the row: each builds the exact_scan.h
+ * aggregates of its slice from the values v in its registers (a chunk is 16
+ * lanes of 4 values: a pair scan over a DPP row; a group is 64 chunks, from
+ * LDS) under binades predicted from the approximate prefix Pb + pk * ce[c],
+ * stores them and the values in the row's fallback region and signals on
+ * sync[sw]; workgroup 0 then walks the row (resolve) and publishes the running
+ * value after the threshold element (has_thr) or after the last, and the
+ * position, in its words pw and pw + 1.  The stores are plain: each workgroup
+ * waits for them and makes them visible at agent scope before it signals, and
+ * the walker acquires after the signals are in.  Every workgroup returns the
+ * same (pos, value), or false when a wait gave up (status flagged, misc[6]). */
+template <uint32_t LIMIT, int EPT>
+__device__ __forceinline__ bool split_sum53(const float (&v)[EPT], double Pb, double pk, const double *ce,
+                                            const FullParams &f, int row, int g, int s0, int s1, bool has_thr,
+                                            double thr, int sw, int pw, uint32_t *sync, uint64_t *pubrow,
+                                            uint64_t *la0, uint64_t *la1, int *lbh, int *misc, double *md,
+                                            int &pos, double &value) {
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id(), T = kFullThreads;
+    const int V = f.p.V, G = f.G;
+    unsigned char *fbr = f.fb + (int64_t)row * f.fb_bytes;
+    const Aggs A = make_aggs(fbr, V);
+    float *qb = (float *)(fbr + f.fb_q_off);
+    const int nchr = (V + 63) >> 6, ngr = (nchr + 63) >> 6, cb0 = s0 >> 6;
+#pragma unroll
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int u = t + j4 * T, lc = u >> 4;
+        if (s0 + 4 * u < s1) *(float4 *)&qb[s0 + 4 * u] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+        const int bs = predict_binade<53>(Pb + pk * ce[lc]);
+        const int be = predict_binade<53>(Pb + pk * ce[lc + 1]);
+        const int ue = bs - 52;
+        Pair x = increment(v[4 * j4], ue);
+        x = compose(x, increment(v[4 * j4 + 1], ue));
+        x = compose(x, increment(v[4 * j4 + 2], ue));
+        x = compose(x, increment(v[4 * j4 + 3], ue));
+        x = compose(dpp_pair<kDppRowShr1>(x), x);
+        x = compose(dpp_pair<kDppRowShr2>(x), x);
+        x = compose(dpp_pair<kDppRowShr4>(x), x);
+        x = compose(dpp_pair<kDppRowShr8>(x), x);
+        if ((lane & 15) == 15) {
+            const int b = bs == be ? bs : kInvalidBinade;
+            la0[lc] = x.a0; la1[lc] = x.a1; lbh[lc] = b;
+            if (cb0 + lc < nchr) { A.a0[cb0 + lc] = x.a0; A.a1[cb0 + lc] = x.a1; A.bh[cb0 + lc] = b; }
+        }
+    }
+    __syncthreads();
+    for (int lg = w; lg < EPT / 4; lg += T / 64) {
+        const int gg = (s0 >> 12) + lg;
+        if (gg >= ngr) continue;
+        const int c = lg * 64 + lane;
+        const bool in = cb0 + c < nchr;
+        const int b0 = lbh[lg * 64];
+        if (ballot(in && lbh[c] != b0) != 0 || b0 == kInvalidBinade) {
+            if (lane == 0) A.gbh[gg] = kInvalidBinade;
+            continue;
+        }
+        Pair x = in ? Pair{la0[c], la1[c]} : Pair{0, 0};
+        x = wave_incl_scan(x, lane);
+        if (lane == 63) { A.ga0[gg] = x.a0; A.ga1[gg] = x.a1; A.gbh[gg] = b0; }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(&sync[sw], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (w == 0) {
+        uint64_t wv = kReady | 0x7ff8000000000000ull, wp = kReady;
+        uint32_t spins = 0;
+        bool got = true;
+        if (g == 0) {
+            while (at_ld32(&sync[sw]) < (uint32_t)G)
+                if (++spins > LIMIT) { got = false; break; }
+            if (got) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                const ResolveOut<53> o = resolve<53>(V, QRow{qb}, A, has_thr, thr);
+                wv = d2u(o.value) | kReady;
+                wp = (uint64_t)(uint32_t)o.pos | kReady;
+            }
+            if (lane == 0) { at_st64(&pubrow[pw + 1], wp); at_st64(&pubrow[pw], wv); }
+        } else {
+            while (!((wv = at_ld64(&pubrow[pw])) & kReady))
+                if (++spins > LIMIT) { got = false; break; }
+            if (got) wp = at_ld64(&pubrow[pw + 1]);
+        }
+        if (lane == 0) {
+            const double val = u2d(wv & ~kReady);
+            if (!got) {
+                if (f.p.status) atomicOr(f.p.status, DLK_STATUS_SYNC_TIMEOUT);
+                misc[6] = 1;
+            }
+            misc[31] = got && !__builtin_isnan(val);
+            misc[30] = (int)(uint32_t)wp;
+            md[2] = val;
+        }
+    }
+    __syncthreads();
+    pos = misc[30];
+    value = md[2];
+    const bool ok = misc[31] != 0;
+    __syncthreads();
+    return ok;
+}
+
 /* NOWAIT (a test instance): every wait gives up at its first poll that finds a
  * word not yet written, which sets DLK_STATUS_SYNC_TIMEOUT. */
 template <int EPT, bool CAP, bool NOWAIT = false>
@@ -482,7 +593,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const float inv_a = (float)(1.0 / (Sapx * (1.0 + eps_s)));
     const float inv_b = (float)(1.0 / (Sapx * (1.0 - eps_s)));
     bool ok = inv_a == inv_b && !f.force_exact;
-    const float inv = inv_a;
+    float inv = inv_a;
+    if (DLK_COLD((inv_a != inv_b || f.force_exact == 2) && f.force_exact != 1 && !p.minp_on && !misc[6])) {
+        /* the bound straddles a float rounding boundary: the sequential sum
+         * itself, split over the row's workgroups */
+        double Eb = 0.0;
+        for (int h = 0; h < g; h++) Eb += u2d(pc[h * kPubWords + kPubE]);
+        int pos;
+        double s1v;
+        ok = split_sum53<kLimit, EPT>(v, Eb, 1.0, ce, f, row, g, s0, s1, false, 0.0, kSyncSplitE, kPubSplitE, sync,
+                                      pubrow, rtot, rpre, cbh, misc, md, pos, s1v);
+        inv = (float)(1.0 / s1v);
+    }
 
     float inv3 = 1.0f;
     int x = V - 1;
@@ -726,6 +848,17 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             x = (int)xw;
             inv3 = u2f((uint32_t)misc[11]);
             __syncthreads();
+        }
+        if (DLK_COLD(topp && p.top_p > 0.0f && !p.minp_on && (!ok || f.force_exact == 2) && !misc[6])) {
+            /* the cut or its normaliser is undecided: the cumulation itself
+             * (src/sampler.c:207-215), split over the row's workgroups; no
+             * crossing keeps every entry (nk = k) */
+            int pos;
+            double s3;
+            ok = split_sum53<kLimit, EPT>(v, RWg, (double)pk, ce, f, row, g, s0, s1, true, p.topp_thr, kSyncSplitP,
+                                          kPubSplitP, sync, pubrow, rtot, rpre, cbh, misc, md, pos, s3);
+            x = pos >= 0 ? pos : V - 1;
+            inv3 = (float)(1.0 / s3);
         }
     }
 

@@ -75,6 +75,9 @@ typedef struct {
                                    DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid).
                                    Shapes whose slices hold 16 entries per thread, no soft-cap;
                                    others return DLK_ERR_UNSUPPORTED */
+#define DLK_PATH_FULL_SPLIT 4  /* fused full-vocabulary kernel that finds the softmax sum and the top-p cut
+                                  of every row by its split exact sums, as it does for a row whose
+                                  certified bounds do not decide them (tests) */
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */
