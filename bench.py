@@ -42,7 +42,7 @@ def fused_kernel_name(rows: int, vocab: int) -> str:
 # The dominant kernel of each workload and its committed traffic summary.
 DOMINANT = {"C1": ("dlk::topk_kernel<false, false>", None),
             "C3": ("dlk::topk_kernel<false, false>", "topk_kernel_c3"),
-            "C4": ("dlk::dfa_mask_kernel", None),
+            "C4": ("dlk::dfa_walk_kernel<16>", None),
             "C5": ("dlk::topk_kernel<false, false>", "topk_kernel_c5"),
             "C5CAP": ("dlk::topk_kernel<true, false>", None),
             "CAP": ("dlk::softcap_vec_kernel", "softcap_vec_kernel_cap")}

@@ -7,11 +7,12 @@
  * bytes from the current state.
  *
  * Two kernels.  Automata of up to 64 states (dfa_walk_kernel): a wave's lanes
- * are the rows (their start states) and the tokens are shared by the wave, so
- * every step of every lane reads the same row of a byte-major table -- one LDS
- * row of 68 bytes, no bank conflicts -- and the token's bytes come from LDS as
- * broadcast reads.  Larger automata (dfa_mask_kernel): one thread per token
- * walking it for every row of its row group.
+ * are the distinct start states of the rows (rows in one state share one mask,
+ * so a batch of any size walks at most 64 of them) and the tokens are shared by
+ * the wave, so every step of every lane reads the same row of a byte-major
+ * table -- one LDS row of 68 bytes, no bank conflicts -- and the token's bytes
+ * come from LDS as broadcast reads.  Larger automata (dfa_mask_kernel): one
+ * thread per token walking it for every row of its row group.
  */
 #include "dlk_device.h"
 #include "../../../include/diskllm_amd.h"
@@ -135,13 +136,17 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
  * the end entry), both 0 and kWalkAcc absorb, and the token is allowed iff the
  * walk ends at kWalkAcc.  A state is still walking iff its low 6 bits are set.
  *
- * A block covers a range of mask words (32 tokens each) for the RW rows of its
- * row group (grid.y).  It stages its tokens' entry lists in LDS as u16 table
- * offsets c * kWalkNsp, back to back, each closed by the end entry, and the
- * list start of every token (bit 31: not walked -- empty, the EOS id, or past
- * the vocabulary).  Lane l of a wave walks row l % RW for token slot l / RW
- * (64 / RW slots), kWalkTpl tokens at once (independent lookups in flight); the
- * slots' bits are OR-ed across lanes and one lane per row writes the word.
+ * A block covers a range of mask words (32 tokens each) for every row.  The
+ * rows' keys -- the start state if in [0, 64), else 0, which behaves as state 0
+ * (dead, no EOS) -- are collected into a 64-bit set; key index k is the k-th
+ * key of the set, and RW >= the number of keys.  The block stages its tokens'
+ * entry lists in LDS as u16 table offsets c * kWalkNsp, back to back, each
+ * closed by the end entry, and the list start of every token (bit 31: not
+ * walked -- empty, the EOS id, or past the vocabulary).  Lane l of a wave walks
+ * key index l % RW for token slot l / RW (64 / RW slots), kWalkTpl tokens at
+ * once (independent lookups in flight); the slots' bits are OR-ed across lanes
+ * into one word per key, kept in LDS, and the block then writes every row's
+ * words from its key's: a row's kWalkWpb words are one 64-byte line.
  * Walks of one group step together until no lane of the wave is walking: a
  * lane reads past its own end entry into the next lists or the padding of end
  * entries after the last (as long as the block's longest list), harmlessly,
@@ -165,6 +170,10 @@ __device__ __forceinline__ uint32_t live_byte(uint32_t x, int k, uint32_t n_stat
     return v < n_states ? v : 0u;
 }
 
+/* A row's key: its start state if in [0, 64) (a state at or above n_states is
+ * dead but keeps its accept bit for the EOS rule), else 0. */
+DLK_DEV int walk_key(int s) { return s >= 0 && s < 64 ? s : 0; }
+
 template <int RW>
 __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *__restrict__ off,
                                                                 const uint8_t *__restrict__ bytes, int V,
@@ -177,7 +186,9 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     constexpr int TPI = P * kWalkTpl;          /* tokens per wave iteration (divides 32) */
     static_assert(32 % TPI == 0, "an iteration's tokens lie in one mask word");
     extern __shared__ __align__(16) uint8_t sm[];
-    __shared__ uint32_t s_maxlen;
+    __shared__ uint32_t s_maxlen, s_keys[2];
+    __shared__ uint8_t s_key[64];                 /* the state of each key index */
+    __shared__ uint32_t kb[kWalkWpb * 64];        /* [word][key index] */
     uint8_t *tt = sm;
     uint32_t *tpos = (uint32_t *)(sm + kWalkTabBytes);                     /* [kWalkWpb * 32] */
     uint8_t *raw = sm + kWalkTabBytes + kWalkWpb * 32 * 4;                 /* [kWalkRawCap] */
@@ -215,7 +226,7 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
         rb[m] = i < n_raw ? bytes[B + i] : 0u;
     }
     /* ---- LDS: the table byte-major, the bytes, the longest entry list -------- */
-    if (t == 0) s_maxlen = 0;
+    if (t == 0) { s_maxlen = 0; s_keys[0] = 0u; s_keys[1] = 0u; }
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const int i = t + h * kWalkThreads, a = i >> 6, q = i & 63;
@@ -243,7 +254,14 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     }
     __syncthreads();
     if (tk < t1) atomicMax(&s_maxlen, len + 1);
+    for (int r = t; r < n_rows; r += kWalkThreads) {
+        const int kr = walk_key(states[r]);
+        atomicOr(&s_keys[kr >> 5], 1u << (kr & 31));
+    }
     __syncthreads();
+    const uint64_t keys = ((uint64_t)s_keys[1] << 32) | s_keys[0];
+    const int n_keys = __popcll(keys);
+    if (t < 64 && ((keys >> t) & 1ull)) s_key[__popcll(keys & ((1ull << t) - 1ull))] = (uint8_t)t;
     /* ---- each token's entry list: its bytes as table rows, then the end row --- */
     const uint32_t n_ent = n_raw + (uint32_t)(t1 - t0);
     const uint32_t pad = s_maxlen;       /* a walk reads at most this far past a list start */
@@ -257,9 +275,8 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     tpos[t] = (tk >= t1 || len == 0 || tk == eos_id) ? kWalkSkip : p0;
     __syncthreads();
     /* ---- the walks -------------------------------------------------------------- */
-    const int lane = lane_id(), wv = t >> 6, slot = lane / RW;
-    const int r = blockIdx.y * RW + lane % RW;
-    const int s_row = r < n_rows ? states[r] : 0;
+    const int lane = lane_id(), wv = t >> 6, slot = lane / RW, kx = lane % RW;
+    const int s_row = kx < n_keys ? (int)s_key[kx] : 0;
     const uint32_t s_init = (s_row > 0 && s_row < n_states) ? (uint32_t)s_row : 0u;
     const bool eos_ok = s_row > 0 && s_row < 64 && ((accept >> s_row) & 1ull);
     for (int w = w0 + wv; w < w1; w += kWalkThreads / 64) {
@@ -318,7 +335,16 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
 #pragma unroll
         for (int m = RW; m < 64; m <<= 1) bits |= (uint32_t)shfl_xor((int)bits, m);
         if (eos_id >= w * 32 && eos_id < w * 32 + 32 && eos_id < V && eos_ok) bits |= 1u << (eos_id & 31);
-        if (slot == 0 && r < n_rows) out[(int64_t)r * ld + w] = bits;
+        if (slot == 0 && kx < n_keys) kb[(w - w0) * 64 + kx] = bits;
+    }
+    __syncthreads();
+    /* every row's words from its key's: 16 lanes per row, one line each */
+    const int nw = w1 - w0;
+    for (int64_t i = t; i < (int64_t)n_rows * kWalkWpb; i += kWalkThreads) {
+        const int r = (int)(i / kWalkWpb), j = (int)(i % kWalkWpb);
+        if (j >= nw) continue;
+        const int kr = walk_key(states[r]);
+        out[(int64_t)r * ld + w0 + j] = kb[j * 64 + __popcll(keys & ((1ull << kr) - 1ull))];
     }
 }
 
@@ -332,11 +358,11 @@ extern "C" int dlk_dfa_mask(const uint32_t *off, const uint8_t *bytes, int vocab
     if (mask_ld < (vocab + 31) / 32) return DLK_ERR_INVALID;
     if (((uintptr_t)trans & 3) != 0) return DLK_ERR_INVALID;
     if (n_states <= 64) {
-        /* the row-per-lane walk (dfa_walk_kernel) */
+        /* the state-per-lane walk (dfa_walk_kernel): lanes for as many keys as
+         * the rows can hold (at most 64) */
         const int W = (vocab + 31) / 32;
         const int RW = n_rows <= 8 ? 8 : n_rows <= 16 ? 16 : n_rows <= 32 ? 32 : 64;
-        const dim3 grid((unsigned)((W + dlk::kWalkWpb - 1) / dlk::kWalkWpb), (unsigned)((n_rows + RW - 1) / RW));
-        if (grid.y > 65535) return DLK_ERR_UNSUPPORTED;
+        const dim3 grid((unsigned)((W + dlk::kWalkWpb - 1) / dlk::kWalkWpb));
         const size_t lds = dlk::kWalkLds;
         auto launch = [&](const void *fn) -> int {
             static int attr[4] = {0, 0, 0, 0};

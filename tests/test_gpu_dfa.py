@@ -1,9 +1,10 @@
 """GPU parity of dlk_dfa_mask (A16: the byte-DFA allow-mask) with the oracle's
 direct walk (oracle/oracle.c orc_dfa_mask), bit for bit, over the shapes that
-select its kernels and paths: automata of up to 64 states (row-per-lane walk,
-8/16/32/64 rows per wave, several row groups), larger automata (token-per-thread
-walk), the EOS rule, empty tokens, start states outside the automaton, and
-blocks whose tokens are too long to stage in LDS (bytes read from memory)."""
+select its kernels and paths: automata of up to 64 states (state-per-lane walk,
+8/16/32/64 lanes of keys per wave, batches of more rows than states sharing
+masks), larger automata (token-per-thread walk), the EOS rule, empty tokens,
+start states outside the automaton or negative, and blocks whose tokens are
+too long to stage in LDS (bytes read from memory)."""
 import numpy as np
 import pytest
 
@@ -19,7 +20,7 @@ def _announce(msg):
 
 def _expected(d, state, V, n_states):
     """The oracle's walk for a start state inside the automaton; outside it no
-    token is allowed, and the EOS id follows the accept bit (state < 64)."""
+    token is allowed, and the EOS id follows the accept bit (0 < state < 64)."""
     if 0 < state < n_states:
         return O.dfa_mask(d, state, V)
     out = np.zeros((V + 31) // 32, np.uint32)
@@ -40,6 +41,9 @@ CASES = [
     (9000, 40, 200, 0.7, 16, 11, "200 states (token-per-thread kernel)"),
     (9000, 64, 65, 0.6, 16, -1, "65 states (token-per-thread kernel)"),
     (3000, 12, 64, 0.02, 300, 5, "long tokens: unstaged blocks"),
+    (40000, 700, 5, 0.3, 16, 17, "700 rows over 5 states: shared masks"),
+    (262144, 512, 64, 0.7, 16, 262143, "C5 shape: 512 rows, 64 states"),
+    (1000, 9, 40, 0.5, 16, 3, "9 rows: states negative, at 40..63 and above 63"),
 ]
 
 
@@ -63,6 +67,8 @@ def test_dfa_mask_vs_oracle(cuda, case):
     states[rng.random(rows) < 0.1] = 0                                     # dead start
     if rows > 2:
         states[1] = n_states + 1                                           # outside the automaton
+    if rows == 9:
+        states[2:8] = [-1, -70000, 45, 63, 64, 1000]                       # keys 0, 45, 63, 0, 0
     _announce(f"dfa {label}: V={V} rows={rows} n_states={n_states}")
     got = api.dfa_masks(off, data, trans, states, V, eos, accept).cpu().numpy().view(np.uint32)
     for r in range(rows):
