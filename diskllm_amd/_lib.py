@@ -22,7 +22,7 @@ DLK_ERR_FORMAT = -4
 DLK_STATUS_HISTORY_TOO_LONG = 1
 DLK_STATUS_SYNC_TIMEOUT = 2
 DLK_STATUS_UNSUPPORTED_ROW = 4
-PATH_AUTO, PATH_ROW, PATH_FULL_EXACT, PATH_FULL_NO_WAIT, PATH_FULL_SPLIT = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_ROW, PATH_FULL_EXACT, PATH_FULL_NO_WAIT = 0, 1, 2, 3
 
 OP_REPETITION, OP_FREQUENCY, OP_PRESENCE = 1, 2, 3
 ORDER_REFERENCE = OP_PRESENCE | (OP_REPETITION << 4)

@@ -335,9 +335,10 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     int rows_per = cap / G;
     if (rows_per < 1) return 1;
     if (rows_per > rows) rows_per = rows;
-    /* per row: the fallback's aggregates, then the row's values for the split sums */
+    /* per row: the fallback's aggregates, then the row's values for the split
+     * sums (V) or one slice's for a re-walked draw (S, which may exceed V) */
     const size_t fb_q_off = r16(aggs_bytes(vocab));
-    const size_t fb_bytes = fb_q_off + r16((size_t)vocab * 4);
+    const size_t fb_bytes = fb_q_off + r16((size_t)(vocab > S ? vocab : S) * 4);
     const size_t n_ln = r16((size_t)rows_per * G * kLaneWords * 8);
     WsView ws;
     /* the published words live in the zeroed counter region: they are zero
@@ -479,11 +480,10 @@ int sample_impl(const dlk_batch *b, int rows, int vocab, const dlk_sample_params
         int rc = launch_topk(p, rows, vocab, stream);
         if (rc <= 0) return rc;
     }
-    if ((prm->path == DLK_PATH_AUTO || prm->path == DLK_PATH_FULL_EXACT || prm->path == DLK_PATH_FULL_NO_WAIT ||
-         prm->path == DLK_PATH_FULL_SPLIT) &&
+    if ((prm->path == DLK_PATH_AUTO || prm->path == DLK_PATH_FULL_EXACT || prm->path == DLK_PATH_FULL_NO_WAIT) &&
         !p.greedy && !p.topk_on) {
-        const int force = prm->path == DLK_PATH_FULL_EXACT ? 1 : prm->path == DLK_PATH_FULL_SPLIT ? 2 : 0;
-        int rc = launch_full(p, rows, vocab, force, prm->path == DLK_PATH_FULL_NO_WAIT, stream);
+        int rc = launch_full(p, rows, vocab, prm->path == DLK_PATH_FULL_EXACT, prm->path == DLK_PATH_FULL_NO_WAIT,
+                             stream);
         if (rc <= 0) return rc;
     }
     if (total > kMaxLds) return DLK_ERR_UNSUPPORTED;

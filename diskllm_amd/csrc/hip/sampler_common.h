@@ -45,8 +45,7 @@ struct Row {
 
 /* The logit sampler_sample sees: soft-capped (src/core/context.c:873-876), then
  * the mask's -INFINITY (src/core/grammar.c:285-305), then the penalties. */
-DLK_DEV float prepared(const Row &R, int i) {
-    float x = R.lg[i];
+DLK_DEV float prepared_from(const Row &R, int i, float x) {    /* x: the raw logit R.lg[i] */
     if (R.cap > 0.0f) x = dlk_softcap_glibc(x, R.cap);
     if (R.mk && !((R.mk[i >> 5] >> (i & 31)) & 1u)) x = -INFINITY;
     if (R.np && ((R.pflag[i >> 11] >> ((i >> 6) & 31)) & 1u)) {
@@ -60,6 +59,7 @@ DLK_DEV float prepared(const Row &R, int i) {
     }
     return x;
 }
+DLK_DEV float prepared(const Row &R, int i) { return prepared_from(R, i, R.lg[i]); }
 
 DLK_DEV float scaled(const Row &R, int i) { return (prepared(R, i) - R.M) * R.inv_t; }
 DLK_DEV float expo(const Row &R, float s) { return dlk_expf_glibc(s - R.maxv, R.tab); }

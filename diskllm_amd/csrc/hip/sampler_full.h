@@ -20,7 +20,8 @@ enum : int {
     kSyncExit = 3,     /* workgroups finished */
     kSyncLanes = 5,    /* workgroups that published their candidate chains */
     kSyncSplitE = 6,   /* workgroups that stored their slice of the split softmax sum */
-    kSyncSplitP = 7    /* workgroups that stored their slice of the split top-p cumulation */
+    kSyncSplitP = 7,   /* workgroups that stored their slice of the split top-p cumulation */
+    kSyncSplitM = 8    /* workgroups that stored their slice of the split min-p survivors' sum */
 };
 
 /* published words per workgroup */
@@ -31,6 +32,8 @@ enum : int {
     kPubS2 = 3,        /* min-p: double, slice sum of the surviving p */
     kPubA2 = 4,        /* min-p: double, slice sum of every p */
     kPubN2 = 5,        /* min-p: surviving entries in the slice */
+    kPubSplitM = 6,    /* workgroup 0: the split min-p survivors' sum (double bits; NaN: a wait gave
+                          up); word 7 its (unused) position */
     kPubP0 = 8,        /* float bits of p_0 (workgroup 0) */
     kPubF = 9,         /* double: the slice's predicted contribution to the draw's float sum */
     kPubX = 10,        /* from the slice holding the top-p crossing: x (bits 0-30, 0x7fffffff: not
@@ -55,10 +58,12 @@ struct FullParams {
                           (low word) and crossing token (high word: -1 none, -2 unresolved);
                           word 64: float bits of candidate 0 */
     unsigned char *fb; /* [rows][fb_bytes]: global aggregates for the exact fallback and the split
-                          sums, then (at fb_q_off) the row's values for the split sums */
+                          sums, then (at fb_q_off) the row's values for the split sums or a slice's
+                          for a re-walked draw */
     size_t fb_bytes, fb_q_off;
-    int force_exact;   /* test hooks: 1 sends every row through the exact fallback; 2 runs the
-                          split sums on every row (as if neither bound had decided) */
+    int force_exact;   /* test hook: every row runs the split sums (as if no bound had decided
+                          them) and re-walks the draw of every slice from its exact start (as if
+                          no chain covered it) */
     int no_wait;       /* test hook: launch the instance whose waits give up at their first poll
                           that finds a word not yet written (DLK_STATUS_SYNC_TIMEOUT) */
 };

@@ -6,8 +6,9 @@
  * dlk_launch_full_kernel); each keeps its slice in registers.  The row is
  * tied together by four row barriers through relaxed agent-scope atomics
  * (every shared word is an atomic store/load; each writer waits for its stores
- * before it signals, so no cache-flushing fences are needed), and finished by
- * the last workgroup to arrive:
+ * before it signals, so no cache-flushing fences are needed on this path; only
+ * the split sums' bulk stores take an agent-scope release and acquire), and
+ * finished by the last workgroup to arrive:
  *
  *   A  slice maxima            -> M (src/sampler.c:155-158)
  *   B  slice sums of e         -> inv = (float)(1/sum), certified: the sequential
@@ -25,10 +26,13 @@
  *         prediction; the last workgroup of the row composes the slices from the
  *         row's exact start 0 and writes the token.
  *
- * Rows whose sums cannot be certified (the bound straddles a float rounding
- * boundary; probability ~1e-3 per row), or whose exact start value falls
- * outside a slice's candidates, are finished by one workgroup with the exact
- * sequential emulation of every sum (the general pipeline).
+ * A sum whose bound straddles a float rounding boundary (probability ~1e-3
+ * per row) is found exactly by all G workgroups of the row (split_sum53: the
+ * slices' exact_scan.h aggregates from registers, one walk by workgroup 0),
+ * and the row goes on; a slice whose candidate chains do not cover the value
+ * the composition reaches is walked by the last workgroup itself from that
+ * value (draw_fix), and the composition resumes after it.  Only a wait that
+ * gave up leaves a row undecided (DLK_STATUS_SYNC_TIMEOUT).
  */
 #include "sampler_common.h"
 #include "sampler_full.h"
@@ -275,7 +279,7 @@ struct QRow {
  * waits for them and makes them visible at agent scope before it signals, and
  * the walker acquires after the signals are in.  Every workgroup returns the
  * same (pos, value), or false when a wait gave up (status flagged, misc[6]). */
-template <uint32_t LIMIT, int EPT>
+template <uint32_t LIMIT, int EPT, bool POS = false>
 __device__ __forceinline__ bool split_sum53(const float (&v)[EPT], double Pb, double pk, const double *ce,
                                             const FullParams &f, int row, int g, int s0, int s1, bool has_thr,
                                             double thr, int sw, int pw, uint32_t *sync, uint64_t *pubrow,
@@ -287,17 +291,20 @@ __device__ __forceinline__ bool split_sum53(const float (&v)[EPT], double Pb, do
     const Aggs A = make_aggs(fbr, V);
     float *qb = (float *)(fbr + f.fb_q_off);
     const int nchr = (V + 63) >> 6, ngr = (nchr + 63) >> 6, cb0 = s0 >> 6;
+    /* POS: the positive part of v (the caller negates the entries that count as 0) */
+    auto val = [](float a) { return POS ? (a > 0.0f ? a : 0.0f) : a; };
 #pragma unroll
     for (int j4 = 0; j4 < EPT / 4; j4++) {
         const int u = t + j4 * T, lc = u >> 4;
-        if (s0 + 4 * u < s1) *(float4 *)&qb[s0 + 4 * u] = make_float4(v[4 * j4], v[4 * j4 + 1], v[4 * j4 + 2], v[4 * j4 + 3]);
+        const float q0 = val(v[4 * j4]), q1 = val(v[4 * j4 + 1]), q2 = val(v[4 * j4 + 2]), q3 = val(v[4 * j4 + 3]);
+        if (s0 + 4 * u < s1) *(float4 *)&qb[s0 + 4 * u] = make_float4(q0, q1, q2, q3);
         const int bs = predict_binade<53>(Pb + pk * ce[lc]);
         const int be = predict_binade<53>(Pb + pk * ce[lc + 1]);
         const int ue = bs - 52;
-        Pair x = increment(v[4 * j4], ue);
-        x = compose(x, increment(v[4 * j4 + 1], ue));
-        x = compose(x, increment(v[4 * j4 + 2], ue));
-        x = compose(x, increment(v[4 * j4 + 3], ue));
+        Pair x = increment(q0, ue);
+        x = compose(x, increment(q1, ue));
+        x = compose(x, increment(q2, ue));
+        x = compose(x, increment(q3, ue));
         x = compose(dpp_pair<kDppRowShr1>(x), x);
         x = compose(dpp_pair<kDppRowShr2>(x), x);
         x = compose(dpp_pair<kDppRowShr4>(x), x);
@@ -365,6 +372,114 @@ __device__ __forceinline__ bool split_sum53(const float (&v)[EPT], double Pb, do
     const bool ok = misc[31] != 0;
     __syncthreads();
     return ok;
+}
+
+/* The draw's float running sum (src/sampler.c:225-233) over slice h alone from
+ * its exact start value cb (float bits), for the row's last workgroup when the
+ * slice's candidate chains do not cover the value its composition reached.
+ * The slice's final probabilities are recomputed from the logits as the slice
+ * computed them (its patches from the row's history list), the exact_scan.h
+ * aggregates built from registers into LDS (la0/la1/lbh: a chunk per DPP row of
+ * 16 lanes; groups in gm) under binades predicted from cb plus the chunks'
+ * float sums (cs: nch + 1 doubles), the values stored at the row's value
+ * region for the walk's element steps, and wave 0 walks the slice up to x
+ * (resolve).  pos: the first slice index whose running value reaches thr_f,
+ * or -1; endb: the running value's bits after the slice's last entry up to x. */
+template <int EPT, bool CAP>
+__device__ __forceinline__ void draw_fix(const FullParams &f, int row, int h, uint32_t cb, int x, float M, float inv,
+                                         bool keep_all, float inv2, float inv3, float thr_f, Lds &L, const float *lg,
+                                         const uint32_t *mk, double *cs, uint64_t *la0, uint64_t *la1, int *lbh,
+                                         unsigned char *gm, int *misc, int &pos, uint32_t &endb) {
+    const RowParams &p = f.p;
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id(), T = kFullThreads;
+    const int V = p.V, S = f.S, nch = S / 64;
+    const int s0 = h * S, s1 = min(V, s0 + S);
+    const int n = min(s1, x + 1) - s0;
+    Row R;
+    R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.pflag = L.pflag;
+    R.M = M; R.inv_t = p.inv_temp; R.maxv = 0.0f; R.tab = L.tab; R.cap = CAP ? p.cap : 0.0f;
+    R.np = build_patches(p, row, lg, mk, L, p.plan, V);
+    /* each group's values (a thread reads back its own stores below) and the
+     * chunks' float sums, two groups' loads in flight at a time */
+    float *qb = (float *)(f.fb + (int64_t)row * f.fb_bytes + f.fb_q_off);
+#pragma unroll 1
+    for (int jb = 0; jb < EPT / 4; jb += 2) {
+        float4 raw[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int i0 = s0 + 4 * (t + (jb + k) * T);
+            raw[k] = i0 < s1 ? *(const float4 *)(lg + i0) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int u = t + (jb + k) * T, i0 = s0 + 4 * u;
+            const float xs[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+            float q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = i0 + c;
+                const float y = i < s1 ? prepared_from(R, i, xs[c]) : -INFINITY;
+                float v = dlk_expf_glibc_core(fmaxf((y - M) * p.inv_temp, -200.0f), L.tab) * inv;
+                if (p.minp_on) v = keep_all || v >= p.min_p ? v * inv2 : 0.0f;
+                q[c] = i <= x ? (p.topp_on ? v * inv3 : v) : 0.0f;
+            }
+            *(float4 *)&qb[4 * u] = make_float4(q[0], q[1], q[2], q[3]);
+            const float fs = row_scan_f((q[0] + q[1]) + (q[2] + q[3]));
+            if ((lane & 15) == 15) cs[u >> 4] = (double)fs;
+        }
+    }
+    __syncthreads();
+    block_excl_scan(cs, nch, L.red);
+    const double c0 = (double)u2f(cb);
+#pragma unroll 1
+    for (int j4 = 0; j4 < EPT / 4; j4++) {
+        const int u = t + j4 * T, lc = u >> 4;
+        const float4 q4 = *(const float4 *)&qb[4 * u];
+        const int bs = predict_binade<24>(c0 + cs[lc]);
+        const int be = predict_binade<24>(c0 + cs[lc + 1]);
+        const int ue = bs - 23;
+        Pair xp = increment(q4.x, ue);
+        xp = compose(xp, increment(q4.y, ue));
+        xp = compose(xp, increment(q4.z, ue));
+        xp = compose(xp, increment(q4.w, ue));
+        xp = compose(dpp_pair<kDppRowShr1>(xp), xp);
+        xp = compose(dpp_pair<kDppRowShr2>(xp), xp);
+        xp = compose(dpp_pair<kDppRowShr4>(xp), xp);
+        xp = compose(dpp_pair<kDppRowShr8>(xp), xp);
+        if ((lane & 15) == 15) { la0[lc] = xp.a0; la1[lc] = xp.a1; lbh[lc] = bs == be ? bs : kInvalidBinade; }
+    }
+    __syncthreads();
+    uint64_t *ga0 = (uint64_t *)gm, *ga1 = ga0 + 16;
+    int *gbh = (int *)(ga1 + 16);
+    const int nchn = (n + 63) >> 6, ngn = (nchn + 63) >> 6;
+    for (int gi = w; gi < ngn; gi += T / 64) {
+        const int c = gi * 64 + lane;
+        const bool in = c < nchn;
+        const int b0 = lbh[gi * 64];
+        if (ballot(in && lbh[c] != b0) != 0 || b0 == kInvalidBinade) {
+            if (lane == 0) gbh[gi] = kInvalidBinade;
+            continue;
+        }
+        Pair xp = in ? Pair{la0[c], la1[c]} : Pair{0, 0};
+        xp = wave_incl_scan(xp, lane);
+        if (lane == 63) { ga0[gi] = xp.a0; ga1[gi] = xp.a1; gbh[gi] = b0; }
+    }
+    /* the values are read back by wave 0: every store done, the cache lines
+     * this compute unit may hold of the region dropped */
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (w == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        Aggs A;
+        A.a0 = la0; A.a1 = la1; A.bh = lbh; A.ga0 = ga0; A.ga1 = ga1; A.gbh = gbh; A.P = cs;
+        ResolveOut<24> o{-1, u2f(cb)};
+        if (n > 0) o = resolve<24>(n, QRow{qb}, A, true, (double)thr_f, u2f(cb));
+        if (lane == 0) { misc[26] = o.pos; misc[27] = (int)f2u(o.value); }
+    }
+    __syncthreads();
+    pos = misc[26];
+    endb = (uint32_t)misc[27];
+    __syncthreads();
 }
 
 /* NOWAIT (a test instance): every wait gives up at its first poll that finds a
@@ -594,7 +709,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const float inv_b = (float)(1.0 / (Sapx * (1.0 - eps_s)));
     bool ok = inv_a == inv_b && !f.force_exact;
     float inv = inv_a;
-    if (DLK_COLD((inv_a != inv_b || f.force_exact == 2) && f.force_exact != 1 && !p.minp_on && !misc[6])) {
+    if (DLK_COLD((inv_a != inv_b || f.force_exact) && !misc[6])) {
         /* the bound straddles a float rounding boundary: the sequential sum
          * itself, split over the row's workgroups */
         double Eb = 0.0;
@@ -611,6 +726,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const bool topp = p.topp_on;
     double RWg = 0.0;                              /* exact-bounded p prefix before this slice */
     float pk = inv;                                /* prefix of the values at chunk c ~ pk * ce[c] */
+    bool mp_all = true;                            /* min-p: every entry kept (none reaches min_p) */
+    float mp_inv2 = 1.0f;                          /* min-p: the survivors' normaliser */
     if (ok) {
         /* ---- p and the slice's p total (double, any order) ------------------ */
 #pragma unroll
@@ -672,8 +789,38 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             const double Sx = keep_all ? SA : S2;
             const float i2a = (float)(1.0 / (Sx * (1.0 + eps_s)));
             const float i2b = (float)(1.0 / (Sx * (1.0 - eps_s)));
-            if (i2a != i2b) ok = false;
-            const float inv2 = i2a;
+            float inv2 = i2a;
+            if (DLK_COLD((i2a != i2b || f.force_exact) && !misc[6])) {
+                /* the survivors' sum itself (src/sampler.c:198-199), split over
+                 * the row's workgroups: an entry min-p drops adds 0 (negated
+                 * here, the split takes the positive part), predicted from the
+                 * survivors' chunk sums (in Pc, free until the draw) */
+#pragma unroll
+                for (int j = 0; j < EPT; j++)
+                    if (!(keep_all || v[j] >= p.min_p)) v[j] = -v[j];
+#pragma unroll
+                for (int j4 = 0; j4 < EPT / 4; j4++) {
+                    const float d = (fmaxf(v[4 * j4], 0.0f) + fmaxf(v[4 * j4 + 1], 0.0f)) +
+                                    (fmaxf(v[4 * j4 + 2], 0.0f) + fmaxf(v[4 * j4 + 3], 0.0f));
+                    const float fs = row_scan_f(d);
+                    if ((lane & 15) == 15) Pc[(t + j4 * T) >> 4] = (double)fs;
+                }
+                __syncthreads();
+                block_excl_scan(Pc, nch, L.red);
+                double Sb = 0.0;
+                for (int h = 0; h < g; h++) Sb += u2d(pc[h * kPubWords + (keep_all ? kPubA2 : kPubS2)]);
+                int pos;
+                double s2v;
+                ok = split_sum53<kLimit, EPT, true>(v, Sb, 1.0, Pc, f, row, g, s0, s1, false, 0.0, kSyncSplitM,
+                                                    kPubSplitM, sync, pubrow, rtot, rpre, cbh, misc, md, pos, s2v);
+                inv2 = (float)(1.0 / s2v);
+#pragma unroll
+                for (int j = 0; j < EPT; j++) v[j] = fabsf(v[j]);
+            } else if (i2a != i2b) {
+                ok = false;
+            }
+            mp_all = keep_all;
+            mp_inv2 = inv2;
 #pragma unroll
             for (int j = 0; j < EPT; j++) v[j] = keep_all || v[j] >= p.min_p ? v[j] * inv2 : 0.0f;
 #pragma unroll
@@ -849,7 +996,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
             inv3 = u2f((uint32_t)misc[11]);
             __syncthreads();
         }
-        if (DLK_COLD(topp && p.top_p > 0.0f && !p.minp_on && (!ok || f.force_exact == 2) && !misc[6])) {
+        if (DLK_COLD(topp && p.top_p > 0.0f && (!ok || f.force_exact) && !misc[6])) {
             /* the cut or its normaliser is undecided: the cumulation itself
              * (src/sampler.c:207-215), split over the row's workgroups; no
              * crossing keeps every entry (nk = k) */
@@ -862,7 +1009,35 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         }
     }
 
-    bool run_exact = !ok && g == 0;        /* the row's sums could not be certified */
+    /* thread 0 composes from slice h0 and value cb: misc[23] the token
+     * (-1: none up to x), misc[24] the first slice whose chains do not
+     * cover the value reached (-1: none), misc[25] that value */
+    const uint64_t *ent = (const uint64_t *)tab;   /* (the composition's copy of the row's chains) */
+    auto compose = [&](int h0, uint32_t cb) {
+        if (t == 0) {
+            int tk_out = -1, fh = -1;
+            for (int h = h0; h < G && h * S <= x; h++) {
+                if (DLK_COLD(f.force_exact)) { fh = h; break; }
+                uint32_t d = 0;
+                if (h > 0) {
+                    d = cb - (uint32_t)ent[h * kLaneWords + 64];
+                    if (d >= 64u) { fh = h; break; }
+                }
+                const uint64_t e = ent[h * kLaneWords + d];
+                const int tk = (int)(uint32_t)(e >> 32);
+                if (tk == -2) { fh = h; break; }
+                if (tk >= 0) { tk_out = tk; break; }
+                cb = (uint32_t)e;
+            }
+            misc[23] = tk_out;
+            misc[24] = fh;
+            misc[25] = (int)cb;
+        }
+        __syncthreads();
+    };
+    bool run_exact = !ok && g == 0;        /* a wait gave up before the row's sums were decided */
+    bool rewalk = false;                   /* a slice's chains miss the composition's value */
+    float thr_fx = 0.0f;
     if (ok) {
     /* ---- final probabilities, draw aggregates, staged chunks -------------- */
 #pragma unroll
@@ -1283,61 +1458,42 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         /* ---- the last workgroup of the row composes the slices from the
          *      row's exact start 0: slice h's lane for the value slice h-1 ended
          *      with gives slice h's end value or the token ---------------------- */
-        uint64_t *ent = (uint64_t *)tab;
+        uint64_t *entw = (uint64_t *)tab;
         const uint64_t *lrow = f.lanes + (int64_t)row * G * kLaneWords;
-        for (int i = t; i < G * kLaneWords; i += T) ent[i] = at_ld64(&lrow[i]);
+        for (int i = t; i < G * kLaneWords; i += T) entw[i] = at_ld64(&lrow[i]);
         __syncthreads();
-        if (t == 0) {
-            uint32_t cb = 0;
-            int token = -1;
-            bool fail = false;
-            for (int h = 0; h < G && h * S <= x; h++) {
-                uint32_t d = 0;
-                if (h > 0) {
-                    d = cb - (uint32_t)ent[h * kLaneWords + 64];
-                    if (d >= 64u) { fail = true; break; }
-                }
-                const uint64_t e = ent[h * kLaneWords + d];
-                const int tk = (int)(uint32_t)(e >> 32);
-                if (tk == -2) { fail = true; break; }
-                if (tk >= 0) { token = tk; break; }
-                cb = (uint32_t)e;
-            }
-            /* nothing crossed r up to x: the last kept entry (src/sampler.c:233) */
-            if (!fail && token < 0) token = x;
-            misc[23] = fail ? -1 : token;
-        }
-        __syncthreads();
-        if (misc[23] >= 0) {
-            if (t == 0) p.out_ids[row] = misc[23];
-        } else {
-            run_exact = true;
-        }
+        compose(0, 0u);
+        /* nothing crossed r up to x: the last kept entry (src/sampler.c:233) */
+        int token = misc[23] >= 0 ? misc[23] : x;
+        rewalk = misc[24] >= 0;
+        thr_fx = thr_f;
+        if (DLK_HOT(!rewalk) && t == 0) p.out_ids[row] = token;
     }
     }
 
-    if (DLK_COLD(run_exact)) {
-        /* ---- exact fallback: one workgroup runs every sum sequentially-exact -- */
-        int np_row = build_patches(p, row, lg, mk, L, p.plan, V);
-        Row R;
-        R.lg = lg; R.mk = mk; R.V = V; R.pid = L.pid; R.pval = L.pval; R.np = np_row; R.pflag = L.pflag;
-        R.M = M; R.inv_t = inv_t; R.maxv = 0.0f; R.tab = L.tab; R.cap = p.cap;
-        FullBase fb{&R};
-        Scal Sc;
-        int pos = pipeline(p, fb, V, r, f.fb + (int64_t)row * f.fb_bytes, L, Sc);
-        /* after a wait gave up (the row is flagged invalid in the status word)
-         * the fallback may have run on an incomplete row maximum: the id stays
-         * inside the vocabulary */
-        if (t == 0) p.out_ids[row] = misc[6] && (pos < 0 || pos >= V) ? V - 1 : pos;
-        for (int j = t; j < n_out; j += T) {
-            int64_t o = (int64_t)row * n_out + j;
-            float pj = fb.e(j) * Sc.inv;
-            QDraw<FullBase> qd{&fb, &Sc};
-            float fj = qd(j);
-            if (p.out_cand_ids) p.out_cand_ids[o] = j;
-            if (p.out_cand_probs) p.out_cand_probs[o] = pj;
-            if (p.out_cand_logprobs) p.out_cand_logprobs[o] = fj > 0.0f ? (float)log((double)fj) : -INFINITY;
+    if (DLK_COLD(rewalk)) {
+        /* a slice whose chains do not cover the value the composition reached
+         * is walked itself from that value (draw_fix), and the composition
+         * resumes after it */
+        int token = x;
+        while (true) {
+            const int fh = misc[24];
+            int pos;
+            uint32_t endb;
+            draw_fix<EPT, CAP>(f, row, fh, (uint32_t)misc[25], x, M, inv, mp_all, mp_inv2, inv3, thr_fx, L, lg, mk, Pc,
+                               rtot, rpre, cbh, (unsigned char *)seg, misc, pos, endb);
+            if (pos >= 0) { token = fh * S + pos; break; }
+            if (fh + 1 >= G || (fh + 1) * S > x) break;
+            compose(fh + 1, endb);
+            if (misc[24] < 0) { token = misc[23] >= 0 ? misc[23] : x; break; }
         }
+        if (t == 0) p.out_ids[row] = token;
+    }
+    if (DLK_COLD(run_exact) && t == 0) {
+        /* only a wait that gave up leaves a sum undecided (the status word
+         * flags the launch; the row's id stays inside the vocabulary) */
+        p.out_ids[row] = V - 1;
+        if (p.status) atomicOr(p.status, DLK_STATUS_SYNC_TIMEOUT);
     }
     /* a wait of this workgroup gave up (the status word flags the launch): the
      * row's workgroups may disagree on whether its sums were certified, so no

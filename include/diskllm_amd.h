@@ -69,15 +69,16 @@ typedef struct {
 
 #define DLK_PATH_AUTO 0        /* fastest path that covers the configuration */
 #define DLK_PATH_ROW 1         /* one workgroup per row, every sum emulated exactly */
-#define DLK_PATH_FULL_EXACT 2  /* fused full-vocabulary kernel with every row finished by its exact fallback */
+#define DLK_PATH_FULL_EXACT 2  /* fused full-vocabulary kernel with every row finished by its exact
+                                  fallbacks: the softmax, min-p and top-p sums found by the split exact
+                                  sums and the draw walked slice by slice from each slice's exact start,
+                                  as for a row whose certified bounds or candidate chains do not decide
+                                  them (tests) */
 #define DLK_PATH_FULL_NO_WAIT 3  /* fused full-vocabulary kernel whose cross-workgroup waits give up at the
                                    first poll that finds a word not yet written: forces the
                                    DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid).
                                    Shapes whose slices hold 16 entries per thread, no soft-cap;
                                    others return DLK_ERR_UNSUPPORTED */
-#define DLK_PATH_FULL_SPLIT 4  /* fused full-vocabulary kernel that finds the softmax sum and the top-p cut
-                                  of every row by its split exact sums, as it does for a row whose
-                                  certified bounds do not decide them (tests) */
 
 typedef struct {
     const float *logits;      /* [rows, ld] fp32, read only */
