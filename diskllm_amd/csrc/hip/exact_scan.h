@@ -177,6 +177,36 @@ DLK_DEV Pair wave_incl_scan(Pair x, int lane) {
     return x;
 }
 
+/* The pair of a 64-element chunk held by a 16-lane row, four values per lane
+ * in order (q0..q3, non-negative floats), on the grid 2^ue: every lane gets
+ * the inclusive composition of its row's increments, lane 15 the chunk's.
+ * When no value of the wave lies exactly halfway between two grid points, no
+ * increment depends on the running value's parity: the pair is (n, n) with n
+ * the sum of the values rounded to the grid, taken in double (exact while
+ * below 2^53; a sum at or past 2^53 is past any binade's top, so it only has
+ * to stay there, and is saturated at kCap).  Otherwise the wave composes the
+ * pairs (increment()). */
+DLK_DEV Pair row_chunk_pair(float q0, float q1, float q2, float q3, int ue) {
+    const double d0 = ldexp((double)q0, -ue), d1 = ldexp((double)q1, -ue);
+    const double d2 = ldexp((double)q2, -ue), d3 = ldexp((double)q3, -ue);
+    const double n0 = rint(d0), n1 = rint(d1), n2 = rint(d2), n3 = rint(d3);
+    const bool tie = fabs(d0 - n0) == 0.5 || fabs(d1 - n1) == 0.5 || fabs(d2 - n2) == 0.5 || fabs(d3 - n3) == 0.5;
+    if (ballot(tie) == 0) {
+        const double sum = row_scan_d((n0 + n1) + (n2 + n3));
+        const uint64_t a = sum >= 0x1p62 ? kCap : (uint64_t)sum;
+        return Pair{a, a};
+    }
+    Pair x = increment(q0, ue);
+    x = compose(x, increment(q1, ue));
+    x = compose(x, increment(q2, ue));
+    x = compose(x, increment(q3, ue));
+    x = compose(dpp_pair<kDppRowShr1>(x), x);
+    x = compose(dpp_pair<kDppRowShr2>(x), x);
+    x = compose(dpp_pair<kDppRowShr4>(x), x);
+    x = compose(dpp_pair<kDppRowShr8>(x), x);
+    return x;
+}
+
 /* Aggregates of one sequence: chunk (64) and group (4096) level.  Flat
  * pointers, so they may live in LDS or in global memory. */
 struct Aggs {

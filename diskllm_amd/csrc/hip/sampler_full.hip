@@ -437,15 +437,7 @@ __device__ __forceinline__ void draw_fix(const FullParams &f, int row, int h, ui
         const float4 q4 = *(const float4 *)&qb[4 * u];
         const int bs = predict_binade<24>(c0 + cs[lc]);
         const int be = predict_binade<24>(c0 + cs[lc + 1]);
-        const int ue = bs - 23;
-        Pair xp = increment(q4.x, ue);
-        xp = compose(xp, increment(q4.y, ue));
-        xp = compose(xp, increment(q4.z, ue));
-        xp = compose(xp, increment(q4.w, ue));
-        xp = compose(dpp_pair<kDppRowShr1>(xp), xp);
-        xp = compose(dpp_pair<kDppRowShr2>(xp), xp);
-        xp = compose(dpp_pair<kDppRowShr4>(xp), xp);
-        xp = compose(dpp_pair<kDppRowShr8>(xp), xp);
+        const Pair xp = row_chunk_pair(q4.x, q4.y, q4.z, q4.w, bs - 23);
         if ((lane & 15) == 15) { la0[lc] = xp.a0; la1[lc] = xp.a1; lbh[lc] = bs == be ? bs : kInvalidBinade; }
     }
     __syncthreads();
