@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X sampling path on its headline configuration.
 
-Workload C2: fp32 logits [64, 151936] (Qwen vocab),
+Workload C2 (the headline configuration): fp32 logits [64, 151936] (Qwen vocab),
 N(0,2^2) + Zipf(1.1) rank bias, repetition 1.15 / frequency 0.3 / presence 0.5
 over a 256-id Zipf history, temperature 1.0, top-p 0.9, no top-k -- one
 dlk_sample() call over the batch is one step.  Inputs are resident in HBM before
