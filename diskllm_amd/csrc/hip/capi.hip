@@ -93,7 +93,7 @@ struct WsView {
  * host code `scratch` names a host-side stand-in, never the device memory: the
  * device address comes from hipGetSymbolAddress, once per device, with that
  * device current (scratch_ptr), and only that address is handed to kernels. */
-constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr size_t kScratchBytes = (size_t)DLK_NOALLOC_SCRATCH_BYTES;
 constexpr size_t kScratchCtrWords = (size_t)1 << 16;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 unsigned char *g_scratch_dev[64];     /* per device: the address of its copy */
@@ -339,6 +339,13 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
      * sums (V) or one slice's for a re-walked draw (S, which may exceed V) */
     const size_t fb_q_off = r16(aggs_bytes(vocab));
     const size_t fb_bytes = fb_q_off + r16((size_t)(vocab > S ? vocab : S) * 4);
+    if (g_noalloc) {
+        /* the fixed scratch array: as many rows per launch as it holds */
+        const size_t room = kScratchBytes - kScratchCtrWords * 4 - 256;
+        const size_t per = fb_bytes + (size_t)G * kLaneWords * 8;
+        if (room / per < (size_t)rows_per) rows_per = (int)(room / per);
+        if (rows_per < 1) return DLK_ERR_UNSUPPORTED;
+    }
     const size_t n_ln = r16((size_t)rows_per * G * kLaneWords * 8);
     WsView ws;
     /* the published words live in the zeroed counter region: they are zero

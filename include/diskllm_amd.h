@@ -119,14 +119,16 @@ int dlk_release_stream(hipStream_t stream);
 /* dlk_sample without any allocation.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops and harnesses that forbid hipMalloc).  Same arguments, kernels
- * and results as dlk_sample; its workspace is a fixed 32 MiB scratch array per
+ * and results as dlk_sample; its workspace is a fixed 64 MiB scratch array per
  * device (held until the process ends), whose counter words each call clears
  * with a fill kernel on `stream`.  Every call on a device shares that device's
  * array, so calls that overlap on one device race.  DLK_ERR_UNSUPPORTED when the
  * call needs more than the array holds or a second buffer: max_history > 1024
  * (the penalties then run on a scratch copy of the rows), or a batch whose
- * kernels' workspace exceeds the array. */
-#define DLK_NOALLOC_SCRATCH_BYTES (32u << 20)
+ * kernels' workspace exceeds the array (the fused full-vocabulary kernel takes
+ * as many rows per launch as the array holds, about 680 KB per row at a
+ * vocabulary of 151,936). */
+#define DLK_NOALLOC_SCRATCH_BYTES (64u << 20)
 int dlk_sample_noalloc(const dlk_batch *batch, int rows, int vocab, const dlk_sample_params *params,
                        hipStream_t stream);
 
