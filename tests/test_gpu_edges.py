@@ -236,6 +236,29 @@ def test_split_sums_shapes(cuda, V, rows):
             np.testing.assert_array_equal(a, b, err_msg=f"{w.name}: {key}")
 
 
+@pytest.mark.parametrize("T", [0.5, 0.6, 0.8, 1.3])
+def test_fresh_batches_natural_fallbacks(cuda, T):
+    """Fresh C2 batches through the automatic path at temperatures where rows
+    meet the fused kernel's fallbacks without forcing: sums the certified
+    bounds leave open (split sums) and slices whose candidate chains miss the
+    composition's value (re-walks, mostly at T 0.6 and below).  Every token
+    and rng state against the oracle, over four launches of 64 rows each."""
+    from diskllm_amd import api
+    for b in range(4):
+        w = W.c2(seed=90001 + 131 * b + int(T * 10))
+        w.temperature = T
+        w.name = f"fresh-T{T}-b{b}"
+        print(f"[case] {w.name} rows={w.rows} V={w.vocab}", flush=True)
+        db = api.to_device(w)
+        api.sample(db, api.params_of(w))
+        res = api.results(db)
+        assert res["status"] == 0
+        for r in range(w.rows):
+            o = O.sample_row(O.prepared_row(w, r), int(w.seeds[r]), w.temperature, w.top_k, w.top_p, w.min_p)
+            assert int(res["ids"][r]) == o["token"], (w.name, r, int(res["ids"][r]), o["token"])
+            assert int(res["states"][r]) == o["state"], (w.name, r)
+
+
 @pytest.mark.parametrize("path", [0, 2])
 def test_full_vocab_many_rows(cuda, path):
     """More rows than one cooperative launch holds: the host splits the batch."""
