@@ -32,11 +32,13 @@ METRIC = "sampled rows/sec + achieved HBM GB/s (% of peak), batch 64, vocab 1519
 def fused_kernel_name(rows: int, vocab: int) -> str:
     """Template instance of the fused full-vocabulary kernel dlk_sample launches for
     this shape (the same selection as launch_full in diskllm_amd/csrc/hip/capi.hip:
-    G = ceil(256 / rows) workgroups per row, elements per thread rounded up to a bucket)."""
-    G = min(16, max(1, (256 + rows - 1) // rows))
-    ept = (vocab + G * 1024 - 1) // (G * 1024)
+    G = ceil(512 / rows) workgroups of 512 threads per row, elements per thread
+    rounded up to a bucket; the bench's 256-id histories take the instance that
+    loads one history id per thread)."""
+    G = min(16, max(1, (512 + rows - 1) // rows))
+    ept = (vocab + G * 512 - 1) // (G * 512)
     ept = next(e for e in (16, 24, 32, 40, 48) if ept <= e or e == 48)
-    return f"dlk::full_kernel<{ept}, false, false>"
+    return f"dlk::full_kernel<{ept}, false, false, 1>"
 
 
 # The dominant kernel of each workload and its committed traffic summary.

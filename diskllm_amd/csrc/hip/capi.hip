@@ -20,7 +20,7 @@ extern "C" int dlk_launch_row_kernel(const dlk::RowParams *p, int rows, size_t l
 extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, size_t lds, hipStream_t stream);
 extern "C" int dlk_topk_kernel_occupancy(int kind, size_t lds);
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream);
-extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap);
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap, int hp);
 extern "C" int dlk_launch_long_history_penalties(float *logits, int64_t ld, int rows, int vocab,
                                                  const int32_t *hist_off, const int32_t *hist_ids, uint32_t order,
                                                  float rep, float freq, float pres, int max_hist, int32_t *too_long,
@@ -282,10 +282,11 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     /* min-p with the cut after the first kept entry (it may lie in any slice): the row kernel */
     if (p.minp_on && p.topp_on && p.top_p <= 0.0f) return 1;
     if (!(p.inv_temp < INFINITY)) return 1;            /* (v - M) * inv_t is NaN at the maximum */
-    if (p.plan.hcap > T) return 1;                     /* one history id per thread, loaded first */
+    if (p.plan.hcap > 2 * T) return 1;                 /* one or two history ids per thread, loaded first */
     if (((uintptr_t)p.logits & 15) != 0 || (p.ld & 3) != 0) return 1;
     if (vocab < 8192 || (vocab & 3) != 0) return 1;   /* whole 16-byte groups per row */
-    int G = (256 + rows - 1) / rows;
+    /* about 512 workgroups: two per CU on 256 CUs */
+    int G = (512 + rows - 1) / rows;
     if (G > kFullMaxG) G = kFullMaxG;
     if (G < 1) G = 1;
     int ept = (vocab + G * T - 1) / (G * T);
@@ -294,8 +295,8 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     if (G > kFullMaxG) return 1;
     const int S = ept * T;
     if (p.n_out > S) return 1;
-    /* (the no-wait test instance: 16 elements per thread, no soft-cap) */
-    if (no_wait && (ept != 16 || p.cap > 0.0f)) return DLK_ERR_UNSUPPORTED;
+    /* (the no-wait test instance: 24 elements per thread, no soft-cap) */
+    if (no_wait && (ept != 24 || p.cap > 0.0f)) return DLK_ERR_UNSUPPORTED;
     const int nch = S / 64;
     FullParams f;
     memset(&f, 0, sizeof(f));
@@ -304,8 +305,8 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
     f.force_exact = force_exact;
     f.no_wait = no_wait;
     /* carve order of full_kernel: sbits, ce, cbh, ca, rtot, rend, rpre, Pc, smap, svals, spx, elist, elc, seg,
-     * tab, tbase, rres, rbase, pc, misc, md; chunks staged per workgroup: 96 where LDS allows (sharp rows
-     * stage many chunks: every one with a tie and those around r's crossing), else 64 */
+     * tab, tbase, rres, rbase, pc, misc, md; 48 chunks staged per workgroup (sharp rows stage many: every
+     * chunk with a tie and those around r's crossing) */
     auto lds_for = [&](int stage_cap) {
         return fixed_lds(p.plan) + r16((size_t)(S / 32) * 4) + r16((size_t)(nch + 1) * 8) +
                2 * r16((size_t)nch * 4) + r16((size_t)nch * 8) + r16((size_t)nch * 4) + r16((size_t)nch * 8) +
@@ -314,23 +315,24 @@ int launch_full(dlk::RowParams &p, int rows, int vocab, int force_exact, int no_
                r16((size_t)kMaxTabs * 4) + r16((size_t)(kFullThreads / 64) * 64 * 8) +
                r16((size_t)(kFullThreads / 64) * 4) + r16((size_t)G * kPubWords * 8) + r16(64 * 4) + r16(16 * 8);
     };
-    f.stage_cap = lds_for(96) <= kMaxLds ? 96 : 64;
+    f.stage_cap = 48;
     const size_t lds = lds_for(f.stage_cap);
     if (lds > kMaxLds) return 1;
-    /* resident workgroups of this instance: queried once per (device, ept, LDS) */
-    struct CapEntry { int dev, ept; size_t lds; int softcap, cap; };
+    /* resident workgroups of this instance: queried once per (device, ept, LDS, instance) */
+    struct CapEntry { int dev, ept; size_t lds; int softcap, hp, cap; };
     static CapEntry cap_cache[256];       /* fixed, as occ_cache above */
     static int n_cap = 0;
     const int softcap = p.cap > 0.0f ? 1 : 0;
+    const int hp = p.plan.hcap > kFullThreads ? 2 : 1;    /* history ids per thread */
     int dev = 0, cap = -1;
     if (hipGetDevice(&dev) != hipSuccess) return DLK_ERR_HIP;
     for (int i = 0; i < n_cap; i++) {
         const CapEntry &e = cap_cache[i];
-        if (e.dev == dev && e.ept == ept && e.lds == lds && e.softcap == softcap) { cap = e.cap; break; }
+        if (e.dev == dev && e.ept == ept && e.lds == lds && e.softcap == softcap && e.hp == hp) { cap = e.cap; break; }
     }
     if (cap < 0) {
-        cap = dlk_full_kernel_capacity(ept, lds, softcap);
-        if (n_cap < 256) cap_cache[n_cap++] = CapEntry{dev, ept, lds, softcap, cap};
+        cap = dlk_full_kernel_capacity(ept, lds, softcap, hp);
+        if (n_cap < 256) cap_cache[n_cap++] = CapEntry{dev, ept, lds, softcap, hp, cap};
     }
     int rows_per = cap / G;
     if (rows_per < 1) return 1;

@@ -8,7 +8,7 @@
 
 namespace dlk {
 
-constexpr int kFullThreads = 1024;
+constexpr int kFullThreads = 512;    /* two workgroups per CU */
 constexpr int kFullMaxG = 16;        /* workgroups per row */
 constexpr int kPubWords = 16;        /* 64-bit words each workgroup publishes */
 constexpr int kCandSlots = 2;        /* predicted top-p crossing chunks per workgroup */
@@ -43,7 +43,7 @@ enum : int {
                           the next word, its threshold position (-1: none) */
 };
 
-constexpr int kMaxTabs = 48;         /* element-level chunks with a candidate table per workgroup */
+constexpr int kMaxTabs = 32;         /* element-level chunks with a candidate table per workgroup */
 constexpr int kLaneWords = 65;       /* per workgroup: 64 candidate chain results + the window base */
 
 struct FullParams {

@@ -316,7 +316,7 @@ __device__ __forceinline__ bool split_sum53(const float (&v)[EPT], double Pb, do
         }
     }
     __syncthreads();
-    for (int lg = w; lg < EPT / 4; lg += T / 64) {
+    for (int lg = w; lg < EPT * T / 4096; lg += T / 64) {
         const int gg = (s0 >> 12) + lg;
         if (gg >= ngr) continue;
         const int c = lg * 64 + lane;
@@ -476,7 +476,9 @@ __device__ __forceinline__ void draw_fix(const FullParams &f, int row, int h, ui
 
 /* NOWAIT (a test instance): every wait gives up at its first poll that finds a
  * word not yet written, which sets DLK_STATUS_SYNC_TIMEOUT. */
-template <int EPT, bool CAP, bool NOWAIT = false>
+/* HP: history ids per thread (1 up to kFullThreads ids; 2 up to twice that,
+ * an instance of its own so that the common case keeps its registers). */
+template <int EPT, bool CAP, bool NOWAIT = false, int HP = 1>
 __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     constexpr uint32_t kLimit = NOWAIT ? 0u : kFullSpinLimit;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -518,7 +520,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     double *md = (double *)carve(q, 16 * 8);
     if (t < 32) L.tab[t] = kExp2Tab[t];
 
-    /* ---- history first: the row's ids (one per thread; the host keeps the
+    /* ---- history first: the row's ids (HP per thread; the host keeps the
      *      direct history within the workgroup) and, for an id inside this
      *      slice, its logit and mask word, gathered before the bulk loads ----- */
     const int32_t *hist = nullptr;
@@ -527,12 +529,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         hist = p.hist_ids + p.hist_off[row];
         nh = p.hist_off[row + 1] - p.hist_off[row];
     }
-    const int hid = t < nh ? hist[t] : -1;
-    float gx = 0.0f;
-    uint32_t gm = 0xffffffffu;
-    if (hid >= s0 && hid < s1) {
-        gx = lg[hid];
-        if (mk) gm = mk[hid >> 5];
+    int hid[HP];
+    float gx[HP];
+    uint32_t gm[HP];
+#pragma unroll
+    for (int k = 0; k < HP; k++) {
+        hid[k] = t + k * T < nh ? hist[t + k * T] : -1;
+        gx[k] = 0.0f;
+        gm[k] = 0xffffffffu;
+        if (hid[k] >= s0 && hid[k] < s1) {
+            gx[k] = lg[hid[k]];
+            if (mk) gm[k] = mk[hid[k] >> 5];
+        }
     }
 
     /* ---- stream the slice into registers: every load issued before any use */
@@ -540,7 +548,7 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     uint32_t mwd[EPT / 4];
     load_slice<EPT, 0, EPT / 4>(lg, mk, s0, s1, t, T, raw, mwd);
 
-    if (DLK_COLD(nh > p.plan.hcap || nh > T)) {    /* (the host keeps both) */
+    if (DLK_COLD(nh > p.plan.hcap || nh > HP * T)) {    /* (the host keeps both) */
         if (g == 0 && t == 0) {
             p.out_ids[row] = -1;
             if (p.status) atomicOr(p.status, DLK_STATUS_HISTORY_TOO_LONG);
@@ -569,23 +577,31 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     for (int i = t; i < hslots; i += T) { hkey[i] = -1; hcnt[i] = 0u; }
     if (t == 0) { misc[5] = 0; misc[6] = 0; }     /* a NaN / +inf entry; a wait that gave up */
     __syncthreads();
-    int oslot = -1;
-    if (hid >= s0 && hid < s1) {
-        uint32_t h = ((uint32_t)hid * 0x9E3779B1u) >> hshift;
-        for (int probe = 0; probe < hslots; probe++) {
-            const int old = atomicCAS(&hkey[h], -1, hid);
-            if (old == -1) { oslot = (int)h; atomicOr(&sbits[(hid - s0) >> 5], 1u << ((hid - s0) & 31)); }
-            if (old == -1 || old == hid) break;
-            h = (h + 1) & (uint32_t)(hslots - 1);
+    int oslot[HP];
+#pragma unroll
+    for (int k = 0; k < HP; k++) {
+        oslot[k] = -1;
+        const int id = hid[k];
+        if (id >= s0 && id < s1) {
+            uint32_t h = ((uint32_t)id * 0x9E3779B1u) >> hshift;
+            for (int probe = 0; probe < hslots; probe++) {
+                const int old = atomicCAS(&hkey[h], -1, id);
+                if (old == -1) { oslot[k] = (int)h; atomicOr(&sbits[(id - s0) >> 5], 1u << ((id - s0) & 31)); }
+                if (old == -1 || old == id) break;
+                h = (h + 1) & (uint32_t)(hslots - 1);
+            }
+            atomicAdd(&hcnt[h], 1u);
         }
-        atomicAdd(&hcnt[h], 1u);
     }
     __syncthreads();
-    if (oslot >= 0) {
-        float x = gx;
-        if (CAP) x = dlk_softcap_glibc(x, p.cap);
-        if (!((gm >> (hid & 31)) & 1u)) x = -INFINITY;
-        hcnt[oslot] = __float_as_uint(penalize(x, (int)hcnt[oslot], p));
+#pragma unroll
+    for (int k = 0; k < HP; k++) {
+        if (oslot[k] >= 0) {
+            float x = gx[k];
+            if (CAP) x = dlk_softcap_glibc(x, p.cap);
+            if (!((gm[k] >> (hid[k] & 31)) & 1u)) x = -INFINITY;
+            hcnt[oslot[k]] = __float_as_uint(penalize(x, (int)hcnt[oslot[k]], p));
+        }
     }
     /* the patch of a marked id */
     auto hpatch = [&](int id) {
@@ -1497,40 +1513,46 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
 }  // namespace dlk
 
 namespace {
-template <bool CAP>
-const void *full_fn(int which) {
+template <bool CAP, int HP>
+const void *full_fn_hp(int which) {
     using namespace dlk;
     switch (which) {
-        case 0: return (const void *)full_kernel<16, CAP>;
-        case 1: return (const void *)full_kernel<24, CAP>;
-        case 2: return (const void *)full_kernel<32, CAP>;
-        case 3: return (const void *)full_kernel<40, CAP>;
-        default: return (const void *)full_kernel<48, CAP>;
+        case 0: return (const void *)full_kernel<16, CAP, false, HP>;
+        case 1: return (const void *)full_kernel<24, CAP, false, HP>;
+        case 2: return (const void *)full_kernel<32, CAP, false, HP>;
+        case 3: return (const void *)full_kernel<40, CAP, false, HP>;
+        default: return (const void *)full_kernel<48, CAP, false, HP>;
     }
+}
+/* the instance for (elements per thread, soft-cap, history ids per thread) */
+const void *full_fn(int which, int cap, int hp) {
+    if (cap) return hp > 1 ? full_fn_hp<true, 2>(which) : full_fn_hp<true, 1>(which);
+    return hp > 1 ? full_fn_hp<false, 2>(which) : full_fn_hp<false, 1>(which);
 }
 int ept_index(int ept) { return ept == 16 ? 0 : ept == 24 ? 1 : ept == 32 ? 2 : ept == 40 ? 3 : ept == 48 ? 4 : -1; }
 }  // namespace
 
 extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ept, size_t lds, hipStream_t stream) {
     using namespace dlk;
-    static int set[2][5] = {{0, 0, 0, 0, 0}, {0, 0, 0, 0, 0}};
+    static int set[2][2][5];
     static int set_nw = 0;
     const int which = ept_index(ept), cap = f->p.cap > 0.0f ? 1 : 0;
+    const int hp = f->p.plan.hcap > kFullThreads ? 2 : 1;
     if (which < 0) return -1;
-    const void *fn = cap ? full_fn<true>(which) : full_fn<false>(which);
+    const void *fn = full_fn(which, cap, hp);
     if (f->no_wait) {
-        /* the test instance exists for 16 elements per thread, no soft-cap */
-        if (ept != 16 || cap) return -2;
-        fn = (const void *)full_kernel<16, false, true>;
+        /* the test instance exists for 24 elements per thread, no soft-cap */
+        if (ept != 24 || cap || hp != 1) return -2;
+        fn = (const void *)full_kernel<24, false, true>;
         if (!set_nw) {
             if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
             set_nw = 1;
         }
-    } else if (!set[cap][which]) {
+    } else if (!set[cap][hp - 1][which]) {
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return -1;
-        set[cap][which] = 1;
+        set[cap][hp - 1][which] = 1;
     }
-    /* An ordinary launch: the grid fits the device at one workgroup per CU
+    /* An ordinary launch: the grid fits the device's resident workgroups
      * (checked by the host against dlk_full_kernel_capacity), and the row
      * waits only on workgroups of its own row.  Workgroups are dispatched in
      * index order and a row's workgroups are consecutive, so every row below
@@ -1543,11 +1565,11 @@ extern "C" int dlk_launch_full_kernel(const dlk::FullParams *f, int rows, int ep
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap) {
+extern "C" int dlk_full_kernel_capacity(int ept, size_t lds, int cap, int hp) {
     using namespace dlk;
     const int which = ept_index(ept);
     if (which < 0) return 0;
-    const void *fn = cap ? full_fn<true>(which) : full_fn<false>(which);
+    const void *fn = full_fn(which, cap, hp);
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) return 0;
     int per_cu = 0, dev = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kFullThreads, lds) != hipSuccess) return 0;

@@ -77,7 +77,7 @@ typedef struct {
 #define DLK_PATH_FULL_NO_WAIT 3  /* fused full-vocabulary kernel whose cross-workgroup waits give up at the
                                    first poll that finds a word not yet written: forces the
                                    DLK_STATUS_SYNC_TIMEOUT path (tests; the ids are then invalid).
-                                   Shapes whose slices hold 16 entries per thread, no soft-cap;
+                                   Shapes whose slices hold 24 entries per thread, no soft-cap;
                                    others return DLK_ERR_UNSUPPORTED */
 
 typedef struct {
