@@ -177,13 +177,15 @@ def test_long_history_vs_oracle(cuda, n_hist, k):
         assert_rows_match(w, res, list(range(w.rows)))
 
 
-@pytest.mark.parametrize("vocab,n_hist", [(32768, 1000), (151936, 1024), (151936, 700)])
+@pytest.mark.parametrize("vocab,n_hist", [(32768, 1000), (151936, 1024), (151936, 700), (151936, 512),
+                                          (151936, 513)])
 def test_fused_history_hash(cuda, vocab, n_hist):
     """The fused full-vocabulary kernel's history table at its largest direct
     history (up to 1,024 ids; longer ones are applied to a scratch copy first):
     many repeats of few ids (long probe chains), ids on both sides of every
-    slice edge, all-distinct ids; both penalty orders.  Ids and rng states equal
-    the oracle's."""
+    slice edge, all-distinct ids; both penalty orders.  512 ids is the largest
+    history of the instance that loads one id per thread, 513 the smallest of
+    the one that loads two.  Ids and rng states equal the oracle's."""
     rng = np.random.default_rng(vocab + n_hist)
     w = W.c2(rows=4, vocab=vocab)
     edges = [0, vocab - 1] + [e + d for e in range(4096, vocab, 4096) for d in (-1, 0)]
