@@ -484,7 +484,18 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
     const int G = f.G, T = kFullThreads;
-    const int row = blockIdx.x / G, g = blockIdx.x % G;
+    /* a row's workgroups on one XCD: dispatch deals workgroup b to XCD b % 8,
+     * so when the grid holds whole groups of eight rows, the row of b is
+     * 8 (b / 8 / G) + b % 8 and its slice (b / 8) % G */
+    int row, g;
+    if (gridDim.x % (8 * G) == 0) {
+        const int k = blockIdx.x >> 3;
+        row = (k / G) * 8 + (blockIdx.x & 7);
+        g = k % G;
+    } else {
+        row = blockIdx.x / G;
+        g = blockIdx.x % G;
+    }
     const int t = threadIdx.x, lane = lane_id();
     const int V = p.V, S = f.S, nch = S / 64;
     const int s0 = g * S, s1 = min(V, s0 + S);
