@@ -225,6 +225,7 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
         const uint32_t i = (uint32_t)t + (uint32_t)m * kWalkThreads;
         rb[m] = i < n_raw ? bytes[B + i] : 0u;
     }
+    const int st0 = t < n_rows ? states[t] : 0;     /* the first rows' start states, with the other loads */
     /* ---- LDS: the table byte-major, the bytes, the longest entry list -------- */
     if (t == 0) { s_maxlen = 0; s_keys[0] = 0u; s_keys[1] = 0u; }
 #pragma unroll
@@ -253,10 +254,23 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
         if (i < n_raw && i < (uint32_t)kWalkRawCap) raw[i] = (uint8_t)rb[m];
     }
     __syncthreads();
-    if (tk < t1) atomicMax(&s_maxlen, len + 1);
-    for (int r = t; r < n_rows; r += kWalkThreads) {
-        const int kr = walk_key(states[r]);
-        atomicOr(&s_keys[kr >> 5], 1u << (kr & 31));
+    /* the longest entry list and the rows' key set: reduced over each wave
+     * first, then one LDS atomic per wave (512 lanes on one word serialise) */
+    {
+        uint32_t ml = tk < t1 ? len + 1 : 0u;
+        uint64_t ks = 0;
+        for (int r = t; r < n_rows; r += kWalkThreads) ks |= 1ull << walk_key(r == t ? st0 : states[r]);
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            ml = max(ml, (uint32_t)shfl_xor((int)ml, m));
+            ks |= ((uint64_t)(uint32_t)shfl_xor((int)(uint32_t)(ks >> 32), m) << 32) |
+                  (uint32_t)shfl_xor((int)(uint32_t)ks, m);
+        }
+        if ((t & 63) == 0) {
+            atomicMax(&s_maxlen, ml);
+            if ((uint32_t)ks) atomicOr(&s_keys[0], (uint32_t)ks);
+            if ((uint32_t)(ks >> 32)) atomicOr(&s_keys[1], (uint32_t)(ks >> 32));
+        }
     }
     __syncthreads();
     const uint64_t keys = ((uint64_t)s_keys[1] << 32) | s_keys[0];
@@ -268,6 +282,7 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     const bool staged = n_raw <= (uint32_t)kWalkRawCap && (uint64_t)n_ent + pad <= (uint64_t)kWalkStageEntries;
     const uint32_t p0 = b0 - B + (uint32_t)t;
     if (staged) {
+#pragma unroll 4
         for (uint32_t j = 0; j < len; j++) ent[p0 + j] = (uint16_t)(raw[b0 - B + j] * kWalkNsp);
         if (tk < t1) ent[p0 + len] = (uint16_t)(256 * kWalkNsp);
         for (uint32_t i = (uint32_t)t; i < pad; i += kWalkThreads) ent[n_ent + i] = (uint16_t)(256 * kWalkNsp);
