@@ -485,10 +485,22 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
     const RowParams &p = f.p;
     const int G = f.G, T = kFullThreads;
     /* a row's workgroups on one XCD: dispatch deals workgroup b to XCD b % 8,
-     * so when the grid holds whole groups of eight rows, the row of b is
-     * 8 (b / 8 / G) + b % 8 and its slice (b / 8) % G */
+     * so when the grid holds whole groups of eight rows, the rows of b % 8 are
+     * those of XCD b % 8.  Among an XCD's blocks, the first half are the first
+     * block of their CU and the second half the second (two per CU), and the
+     * second block of a CU runs behind the first (older waves win issue): so a
+     * row takes half its slices from each half, rather than all of a row's
+     * slices running behind */
     int row, g;
-    if (gridDim.x % (8 * G) == 0) {
+    if (gridDim.x % (8 * G) == 0 && (G & 1) == 0) {
+        /* k: the block's place among its XCD's blocks; the first and second
+         * halves of them are the first and second block of their CUs: each row
+         * takes G/2 slices from each half */
+        const int k = blockIdx.x >> 3, R = (int)(gridDim.x >> 4), h = G >> 1;
+        const int k2 = k < R ? k : k - R;
+        row = (k2 / h) * 8 + (blockIdx.x & 7);
+        g = (k < R ? 0 : h) + k2 % h;
+    } else if (gridDim.x % (8 * G) == 0) {
         const int k = blockIdx.x >> 3;
         row = (k / G) * 8 + (blockIdx.x & 7);
         g = k % G;
