@@ -490,7 +490,9 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
      * block of their CU and the second half the second (two per CU), and the
      * second block of a CU runs behind the first (older waves win issue): so a
      * row takes half its slices from each half, rather than all of a row's
-     * slices running behind */
+     * slices running behind.  The first half takes slice 0 (the start of the
+     * draw, the row's longest draw phase) and the last G/2 - 1 slices (where
+     * the top-p crossing of a spread-out row lies, which the others wait for) */
     int row, g;
     if (gridDim.x % (8 * G) == 0 && (G & 1) == 0) {
         /* k: the block's place among its XCD's blocks; the first and second
@@ -499,7 +501,8 @@ __global__ __launch_bounds__(kFullThreads) void full_kernel(FullParams f) {
         const int k = blockIdx.x >> 3, R = (int)(gridDim.x >> 4), h = G >> 1;
         const int k2 = k < R ? k : k - R;
         row = (k2 / h) * 8 + (blockIdx.x & 7);
-        g = (k < R ? 0 : h) + k2 % h;
+        const int i = k2 % h;
+        g = k < R ? (i == 0 ? 0 : G - h + i) : 1 + i;
     } else if (gridDim.x % (8 * G) == 0) {
         const int k = blockIdx.x >> 3;
         row = (k / G) * 8 + (blockIdx.x & 7);
