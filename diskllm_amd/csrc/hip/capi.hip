@@ -262,6 +262,7 @@ int launch_topk(dlk::RowParams &p, int rows, int vocab, hipStream_t stream) {
     f.grp_cap = S / 4 < kTopkGroupCap ? S / 4 : kTopkGroupCap;
     f.cand_cap = cc;
     f.buf_cap = cc;
+    f.spread = (int64_t)rows * G >= 4 * (int64_t)n_cu[dev] ? 1 : 0;   /* four or more blocks per CU */
     const size_t lds = lds_for(S, G);
     size_t n_slot = r16((size_t)rows * G * sizeof(TopkSlot));
     size_t n_cand = (size_t)rows * G * KP * 8;

@@ -37,6 +37,9 @@ struct TopkParams {
     int buf_cap;         /* merge buffer entries (LDS) */
     int grp_cap;         /* listed groups per slice (LDS) */
     int cand_cap;        /* slice candidates (LDS) */
+    int spread;          /* 1: grid (rows, G), row blockIdx.x, slice blockIdx.y (a row's slices spread
+                            over the CUs' dispatch slots); 0: grid (G, rows), slice blockIdx.x of row
+                            blockIdx.y */
     uint32_t *counters;  /* [rows], zero between launches */
     TopkSlot *slots;     /* [rows * G] */
     uint64_t *cands;     /* [rows * G * KP] */

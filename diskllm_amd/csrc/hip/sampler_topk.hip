@@ -191,7 +191,13 @@ template <bool CAP, bool GREEDY>
 __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
     extern __shared__ __align__(16) unsigned char smem[];
     const RowParams &p = f.p;
-    const int g = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = lane_id(), w = wave_id();
+    /* With several blocks per CU, the later blocks on a CU stream behind the
+     * earlier ones (older waves win issue and the memory queues): spread,
+     * every row takes its slices from every dispatch slot, rather than the
+     * rows of the last slot all finishing last */
+    const int g = f.spread ? (int)blockIdx.y : (int)blockIdx.x;
+    const int row = f.spread ? (int)blockIdx.x : (int)blockIdx.y;
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int T = kTopkThreads, V = p.V, G = f.G;
     const int s0 = g * f.S, s1 = min(V, s0 + f.S);
     const float *lg = p.logits + (int64_t)row * p.ld;
@@ -930,6 +936,8 @@ extern "C" int dlk_launch_topk_kernel(const dlk::TopkParams *f, int rows, size_t
     }
     TopkParams fp = *f;
     void *args[] = {&fp};
-    if (hipLaunchKernel(fn, dim3(f->G, rows), dim3(kTopkThreads), args, lds, stream) != hipSuccess) return -1;
+    /* blocks are dispatched x-fastest: (rows, G) puts a row's slices a row-count apart */
+    const dim3 grid = f->spread ? dim3(rows, f->G) : dim3(f->G, rows);
+    if (hipLaunchKernel(fn, grid, dim3(kTopkThreads), args, lds, stream) != hipSuccess) return -1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
