@@ -140,8 +140,9 @@ __global__ __launch_bounds__(256) void dfa_mask_kernel(const uint32_t *__restric
  * rows' keys -- the start state if in [0, 64), else 0, which behaves as state 0
  * (dead, no EOS) -- are collected into a 64-bit set; key index k is the k-th
  * key of the set, and RW >= the number of keys.  The block stages its tokens'
- * entry lists in LDS as u16 table offsets c * kWalkNsp, back to back, each
- * closed by the end entry, and the list start of every token (bit 31: not
+ * entry lists in LDS as table offsets c * kWalkNsp, back to back, each
+ * closed by the end entry (each entry held as a u32 together with the next,
+ * so that a step of two entries is one LDS read), and the list start of every token (bit 31: not
  * walked -- empty, the EOS id, or past the vocabulary).  Lane l of a wave walks
  * key index l % RW for token slot l / RW (64 / RW slots), kWalkTpl tokens at
  * once (independent lookups in flight); the slots' bits are OR-ed across lanes
@@ -160,9 +161,9 @@ constexpr int kWalkTplMax = 8;                /* tokens walked at once per lane 
 constexpr int kWalkWpb = kWalkThreads / 32;    /* mask words per block */
 constexpr int kWalkRawPer = 16;                /* token bytes staged per thread (coalesced byte loads) */
 constexpr int kWalkRawCap = kWalkRawPer * kWalkThreads;
-constexpr int kWalkStageEntries = 10240;       /* u16 entries staged per block */
+constexpr int kWalkStageEntries = 10240;       /* entries staged per block (u32 pairs) */
 constexpr uint32_t kWalkSkip = 0x80000000u;
-constexpr size_t kWalkLds = kWalkTabBytes + kWalkWpb * 32 * 4 + kWalkRawCap + kWalkStageEntries * 2;
+constexpr size_t kWalkLds = kWalkTabBytes + kWalkWpb * 32 * 4 + kWalkRawCap + kWalkStageEntries * 4;
 
 /* byte k of x if it is a state of the automaton, else 0 */
 __device__ __forceinline__ uint32_t live_byte(uint32_t x, int k, uint32_t n_states) {
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     uint8_t *tt = sm;
     uint32_t *tpos = (uint32_t *)(sm + kWalkTabBytes);                     /* [kWalkWpb * 32] */
     uint8_t *raw = sm + kWalkTabBytes + kWalkWpb * 32 * 4;                 /* [kWalkRawCap] */
-    uint16_t *ent = (uint16_t *)(raw + kWalkRawCap);                       /* [kWalkStageEntries] */
+    uint32_t *ent = (uint32_t *)(raw + kWalkRawCap);                       /* [kWalkStageEntries] */
     const int t = threadIdx.x;
     const int W = (V + 31) >> 5;
     const int w0 = blockIdx.x * kWalkWpb, w1 = min(W, w0 + kWalkWpb);
@@ -281,11 +282,19 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
     const uint32_t pad = s_maxlen;       /* a walk reads at most this far past a list start */
     const bool staged = n_raw <= (uint32_t)kWalkRawCap && (uint64_t)n_ent + pad <= (uint64_t)kWalkStageEntries;
     const uint32_t p0 = b0 - B + (uint32_t)t;
+    /* each entry together with the next one (the end entry's partner is the
+     * end entry again), so that a step of two entries is one LDS read */
+    constexpr uint32_t kEnd = 256u * kWalkNsp;
     if (staged) {
+        uint32_t cur = len > 0 ? (uint32_t)raw[b0 - B] * kWalkNsp : kEnd;
 #pragma unroll 4
-        for (uint32_t j = 0; j < len; j++) ent[p0 + j] = (uint16_t)(raw[b0 - B + j] * kWalkNsp);
-        if (tk < t1) ent[p0 + len] = (uint16_t)(256 * kWalkNsp);
-        for (uint32_t i = (uint32_t)t; i < pad; i += kWalkThreads) ent[n_ent + i] = (uint16_t)(256 * kWalkNsp);
+        for (uint32_t j = 0; j < len; j++) {
+            const uint32_t nx = j + 1 < len ? (uint32_t)raw[b0 - B + j + 1] * kWalkNsp : kEnd;
+            ent[p0 + j] = cur | (nx << 16);
+            cur = nx;
+        }
+        if (tk < t1) ent[p0 + len] = kEnd | (kEnd << 16);
+        for (uint32_t i = (uint32_t)t; i < pad; i += kWalkThreads) ent[n_ent + i] = kEnd | (kEnd << 16);
     }
     tpos[t] = (tk >= t1 || len == 0 || tk == eos_id) ? kWalkSkip : p0;
     __syncthreads();
@@ -315,8 +324,8 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
                     if (ballot((act & 63u) != 0u) == 0) break;
 #pragma unroll
                     for (int i = 0; i < kWalkTpl; i++) {
-                        const uint32_t e0 = ent[pos[i]], e1 = ent[pos[i] + 1];
-                        st[i] = tt[e1 + tt[e0 + st[i]]];
+                        const uint32_t pr = ent[pos[i]];
+                        st[i] = tt[(pr >> 16) + tt[(pr & 0xffffu) + st[i]]];
                         pos[i] += 2;
                     }
                 }
