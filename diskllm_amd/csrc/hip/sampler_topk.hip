@@ -429,6 +429,9 @@ __global__ __launch_bounds__(kTopkThreads, 8) void topk_kernel(TopkParams f) {
         if (b + 1 < nb) load_batch(xa, ma, b + 1);
     }
 
+    /* several blocks per CU: a slice past its stream takes issue ahead of the
+     * blocks still streaming (which wait on memory), so its tail runs sooner */
+    if (f.spread) __builtin_amdgcn_s_setprio(2);
     float bm;
     int bi = 0x7fffffff, nf = 0, irr = 0, kept = 0, complete = 1;
     uint32_t last_key = 0, fnan = 0;
