@@ -236,6 +236,19 @@ def test_split_sums_shapes(cuda, V, rows):
             np.testing.assert_array_equal(a, b, err_msg=f"{w.name}: {key}")
 
 
+@pytest.mark.parametrize("rows,V", [(16, 151936), (256, 32768), (40, 151936), (24, 151936), (5, 151936)])
+def test_fused_block_to_slice_mappings(cuda, rows, V):
+    """The fused kernel's block -> (row, slice) mappings on the automatic path:
+    16 rows (G 16: a row's slices from both halves of each XCD's blocks), 256
+    rows of a small vocabulary (G 2: one slice from each half), 40 rows (G 13,
+    odd: rows on one XCD, slices in order), 24 rows (G 22: two launches of 23
+    and 1 rows, grids of no whole eight-row groups, consecutive blocks) and 5
+    rows (consecutive blocks).  Tokens and rng states against the oracle."""
+    w = W.c2(seed=100 + rows, rows=rows, vocab=V)
+    w.name = f"mapping-rows{rows}-V{V}"
+    run_and_check(w, 0)
+
+
 @pytest.mark.parametrize("T", [0.5, 0.6, 0.8, 1.3])
 def test_fresh_batches_natural_fallbacks(cuda, T):
     """Fresh C2 batches through the automatic path at temperatures where rows
