@@ -309,9 +309,21 @@ __global__ __launch_bounds__(kWalkThreads) void dfa_walk_kernel(const uint32_t *
         for (int it = 0; it < 32; it += TPI) {
             const int tb = w * 32 + it + slot * kWalkTpl;          /* this lane's first token */
             uint32_t st[kWalkTpl], pos[kWalkTpl];
+            /* the list starts of the lane's tokens, 16 bytes at a time (tb - t0
+             * is a multiple of kWalkTpl, and kWalkTpl of 4) */
+            static_assert(kWalkTpl % 4 == 0, "list starts read four at a time");
+            uint32_t pps[kWalkTpl];
+#pragma unroll
+            for (int i = 0; i < kWalkTpl; i += 4) {
+                const uint4 q4 = *(const uint4 *)&tpos[tb + i - t0];
+                pps[i] = q4.x;
+                pps[i + 1] = q4.y;
+                pps[i + 2] = q4.z;
+                pps[i + 3] = q4.w;
+            }
 #pragma unroll
             for (int i = 0; i < kWalkTpl; i++) {
-                const uint32_t pp = tpos[tb + i - t0];
+                const uint32_t pp = pps[i];
                 pos[i] = pp & ~kWalkSkip;
                 st[i] = (pp & kWalkSkip) ? 0u : s_init;
             }

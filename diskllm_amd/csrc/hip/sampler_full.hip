@@ -1,10 +1,10 @@
 /*
- * sampler_full.hip -- fused full-vocabulary sampling (top-k off, min-p off):
- * src/sampler.c:136-234 with k = V, bit-exact, one HBM pass.
+ * sampler_full.hip -- fused full-vocabulary sampling (top-k off; min-p and
+ * top-p on or off): src/sampler.c:136-234 with k = V, bit-exact, one HBM pass.
  *
- * A row is split over G workgroups, all resident at once (see
- * dlk_launch_full_kernel); each keeps its slice in registers.  The row is
- * tied together by four row barriers through relaxed agent-scope atomics
+ * A row is split over G workgroups of 512 threads, two per CU, all resident at
+ * once (see dlk_launch_full_kernel); each keeps its slice in registers.  The
+ * row is tied together by row barriers through relaxed agent-scope atomics
  * (every shared word is an atomic store/load; each writer waits for its stores
  * before it signals, so no cache-flushing fences are needed on this path; only
  * the split sums' bulk stores take an agent-scope release and acquire), and
@@ -16,9 +16,11 @@
  *                                 relative bound of our sum, and inv is taken only
  *                                 if every value in that interval gives the same
  *                                 float (:182)
- *   C  slice sums of p and the few chunks that can hold the top-p crossing
- *                              -> every workgroup computes the same certified cut x
- *                                 and inv3 (:207-220)
+ *   B2 (min-p) slice sums of the survivors -> inv2, certified as inv is
+ *                                 (:188-202)
+ *   C  slice sums of p -> the slice holding the top-p crossing finds the
+ *                                 certified cut x and inv3 from its candidate
+ *                                 chunks and hands them to the others (:207-220)
  *   D  each slice's predicted contribution to the draw's float running sum
  *                              -> each workgroup's predicted exact start value
  *   last  every workgroup runs the draw's exact float running sum (:226-232,
