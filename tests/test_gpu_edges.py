@@ -236,6 +236,20 @@ def test_split_sums_shapes(cuda, V, rows):
             np.testing.assert_array_equal(a, b, err_msg=f"{w.name}: {key}")
 
 
+@pytest.mark.parametrize("rows,V,k", [(300, 131072, 40), (1030, 65536, 8)])
+def test_topk_slice_major_grid(cuda, rows, V, k):
+    """The top-k kernel's slice-major grid (four or more blocks per CU: grid
+    (rows, G), row blockIdx.x, slice blockIdx.y, raised wave priority for each
+    slice's tail) at row counts that are not multiples of 8, with a history
+    and penalties on every row: tokens, rng states and the candidates against
+    the oracle."""
+    rng = np.random.default_rng(rows)
+    hist = [rng.integers(0, V, 48) for _ in range(rows)]
+    w = make(f"spread-{rows}-{V}", rows, V, seed=rows, temperature=0.9, top_k=k, top_p=0.95, rep=1.2, freq=0.1,
+             pres=0.3, hist=hist, n_out=8)
+    run_and_check(w, 0)
+
+
 @pytest.mark.parametrize("rows,V", [(16, 151936), (256, 32768), (40, 151936), (24, 151936), (5, 151936)])
 def test_fused_block_to_slice_mappings(cuda, rows, V):
     """The fused kernel's block -> (row, slice) mappings on the automatic path:
